@@ -1,0 +1,209 @@
+"""Kernel descriptor API and the select / rank / tune loop.
+
+Mirrors the reference's plugin interface (kernel/autotuner/interface.py):
+``TileLangKernelBase`` with ``name``, ``make_op_spec``, ``get_raw_configs``,
+``raw_config_to_tune_config``, ``score_adjustment``, ``format_config``, and the
+generic ``select_best`` (:136-178) / ``rank_all`` (:181-241).  Descriptors
+written for the reference run unchanged.
+
+Additions for the gfx950 build:
+  * ``prune(configs, hw, **shape)`` hook, applied before scoring.  The default
+    keeps every config (reference behaviour); the MI355X descriptors reject
+    tiles that overflow LDS or VGPRs or under-fill the CUs for the shape.
+  * ``tune(...)``: prune + rank, resolve ("compile") the top-k, benchmark them
+    on the device and return the measured best, with the wall-clock split the
+    reference reports as time-to-best.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Any, Callable, Dict, List, Optional, Tuple
+
+from .cost_model import OpSpec, TuneConfig, score_formula, score_formula_detailed
+from .gpu_spec import GPUSpec, get_gpu_spec
+
+
+class TileLangKernelBase:
+    """Descriptor base class (reference interface.py:50-128).
+
+    Subclasses must override ``name``, ``make_op_spec`` and ``get_raw_configs``.
+    """
+
+    @property
+    def name(self) -> str:
+        raise NotImplementedError
+
+    def make_op_spec(self, raw_config: Optional[Dict[str, Any]] = None, **shape_kwargs: Any) -> OpSpec:
+        raise NotImplementedError
+
+    def get_raw_configs(self, **shape_kwargs: Any) -> List[Dict[str, Any]]:
+        raise NotImplementedError
+
+    # -- defaults ---------------------------------------------------------------
+    def raw_config_to_tune_config(self, raw: Dict[str, Any]) -> TuneConfig:
+        """``thread_num`` -> warps of 32 lanes (reference :92-103)."""
+        return TuneConfig(
+            block_M=raw["block_M"], block_N=raw["block_N"], block_K=raw["block_K"],
+            num_stages=raw["num_stages"], num_warps=raw["thread_num"] // 32,
+        )
+
+    def score_adjustment(self, raw: Dict[str, Any], base_score: float, **shape_kwargs: Any) -> float:
+        return base_score
+
+    def format_config(self, raw: Dict[str, Any]) -> str:
+        """``BM{}_BN{}_BK{}[_SK{}]_S{}_T{}`` (reference :117-128), plus the MFMA
+        wave grid / shape suffix when the config carries one."""
+        parts = [f"BM{raw['block_M']}", f"BN{raw['block_N']}", f"BK{raw['block_K']}"]
+        if "split_k" in raw:
+            parts.append(f"SK{raw['split_k']}")
+        parts.append(f"S{raw['num_stages']}")
+        parts.append(f"T{raw['thread_num']}")
+        if "waves_m" in raw and "waves_n" in raw:
+            parts.append(f"W{raw['waves_m']}x{raw['waves_n']}")
+        if "mfma" in raw:
+            parts.append(f"M{raw['mfma'].split('x')[0]}")
+        return "_".join(parts)
+
+    def prune(self, raw_configs: List[Dict[str, Any]], hw: GPUSpec, **shape_kwargs: Any) -> List[Dict[str, Any]]:
+        return raw_configs
+
+    # -- tune() hooks (device descriptors implement these) ---------------------
+    def make_inputs(self, **shape_kwargs: Any) -> Dict[str, Any]:
+        raise NotImplementedError(f"{self.name} cannot be benchmarked")
+
+    def make_runner(self, raw: Dict[str, Any], inputs: Dict[str, Any], **shape_kwargs: Any) -> Callable[[], Any]:
+        raise NotImplementedError(f"{self.name} cannot be benchmarked")
+
+    def flops(self, **shape_kwargs: Any) -> float:
+        op = self.make_op_spec(**shape_kwargs)
+        return float(op.mainloop.mainloop_flops)
+
+
+def _score(descriptor: TileLangKernelBase, raw, hw, detailed: bool, shape):
+    op = descriptor.make_op_spec(raw_config=raw, **shape)
+    cfg = descriptor.raw_config_to_tune_config(raw)
+    if detailed:
+        detail = score_formula_detailed(op, cfg, hw)
+        base = detail["score"]
+    else:
+        base, detail = score_formula(op, cfg, hw), None
+    return descriptor.score_adjustment(raw, base, **shape), detail
+
+
+def select_best(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None,
+                **shape_kwargs: Any) -> Tuple[Dict[str, Any], float]:
+    """Highest-scoring raw config (strict ``>``: the first of equal scores wins)."""
+    if hw is None:
+        hw = get_gpu_spec()
+    configs = descriptor.prune(descriptor.get_raw_configs(**shape_kwargs), hw, **shape_kwargs)
+    best, best_score = None, -1.0
+    for raw in configs:
+        s, _ = _score(descriptor, raw, hw, False, shape_kwargs)
+        if s > best_score:
+            best, best_score = raw, s
+    if best is None:
+        raise RuntimeError(f"No configs generated for {descriptor.name} with {shape_kwargs}")
+    return best, best_score
+
+
+def rank_all(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, detailed: bool = False,
+             **shape_kwargs: Any) -> List[Dict[str, Any]]:
+    """Every (pruned) config with its score, best first (stable sort)."""
+    if hw is None:
+        hw = get_gpu_spec()
+    configs = descriptor.prune(descriptor.get_raw_configs(**shape_kwargs), hw, **shape_kwargs)
+    out = []
+    for raw in configs:
+        s, detail = _score(descriptor, raw, hw, detailed, shape_kwargs)
+        e = {"raw_config": raw, "score": s, "formatted": descriptor.format_config(raw)}
+        if detailed:
+            e["detail"] = detail
+        out.append(e)
+    out.sort(key=lambda e: e["score"], reverse=True)
+    return out
+
+
+@dataclass
+class TuneResult:
+    best_config: Dict[str, Any]
+    best_ms: float
+    best_tflops: float
+    formula_top1: Dict[str, Any]
+    formula_top1_ms: float
+    candidates: List[Dict[str, Any]] = field(default_factory=list)
+    prune_rank_s: float = 0.0
+    compile_s: float = 0.0
+    bench_s: float = 0.0
+    time_to_best_s: float = 0.0
+    n_configs: int = 0
+    n_pruned: int = 0
+
+    def as_dict(self) -> Dict[str, Any]:
+        return dict(self.__dict__)
+
+
+def benchmark_ms(fn: Callable[[], Any], warmup: int = 3, reps: int = 10, flush_bytes: int = 0) -> float:
+    """Median device time of ``fn`` (HIP events on the current stream)."""
+    import torch
+
+    flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device="cuda") if flush_bytes else None
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        if flush is not None:
+            flush.zero_()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        times.append(s.elapsed_time(e))
+    times.sort()
+    return times[len(times) // 2]
+
+
+def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: int = 4, warmup: int = 2,
+         reps: int = 5, **shape_kwargs: Any) -> TuneResult:
+    """Formula-rank, then measure the top-k on the device and keep the fastest.
+
+    time_to_best = prune+rank (host) + compile (0: instances are AOT) + top-k benchmark.
+    """
+    t0 = time.perf_counter()
+    if hw is None:
+        hw = get_gpu_spec()
+    all_cfgs = descriptor.get_raw_configs(**shape_kwargs)
+    ranked = rank_all(descriptor, hw, **shape_kwargs)
+    if not ranked:
+        raise RuntimeError(f"No configs survive pruning for {descriptor.name} with {shape_kwargs}")
+    t1 = time.perf_counter()
+    inputs = descriptor.make_inputs(**shape_kwargs)
+    runners = [(e, descriptor.make_runner(e["raw_config"], inputs, **shape_kwargs)) for e in ranked[:top_k]]
+    t2 = time.perf_counter()
+    flops = descriptor.flops(**shape_kwargs)
+    cands = []
+    for e, run in runners:
+        ms = benchmark_ms(run, warmup=warmup, reps=reps)
+        cands.append({"config": e["raw_config"], "formatted": e["formatted"], "score": e["score"], "ms": ms,
+                      "tflops": flops / ms / 1e9})
+    t3 = time.perf_counter()
+    best = min(cands, key=lambda c: c["ms"])
+    return TuneResult(
+        best_config=best["config"], best_ms=best["ms"], best_tflops=best["tflops"],
+        formula_top1=cands[0]["config"], formula_top1_ms=cands[0]["ms"], candidates=cands,
+        prune_rank_s=t1 - t0, compile_s=t2 - t1, bench_s=t3 - t2, time_to_best_s=t3 - t0,
+        n_configs=len(all_cfgs), n_pruned=len(all_cfgs) - len(ranked))
+
+
+def configure_autotuner_cache(cache_dir: str = ".icpp_cache") -> None:
+    """Reference :249-261 configures TileLang's JIT cache.  Kernels here are
+    compiled ahead of time into libicpp_hip.so, so there is no cache to set up;
+    kept so callers of the reference API keep working."""
+    return None
+
+
+__all__ = ["TileLangKernelBase", "TuneResult", "benchmark_ms", "configure_autotuner_cache", "rank_all",
+           "select_best", "tune"]

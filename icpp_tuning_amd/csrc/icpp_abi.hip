@@ -1,0 +1,262 @@
+// C ABI of libicpp_hip.so: instance table, argument validation and launchers.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "icpp_registry.hpp"
+
+namespace icpp {
+
+namespace {
+std::vector<Instance>& table(int family) {
+  static std::vector<Instance> t[ICPP_NUM_FAMILIES];
+  return t[family];
+}
+bool& sorted_flag() {
+  static bool s = false;
+  return s;
+}
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+// Instances register from static initializers in unspecified order; present
+// them sorted by name so indices are stable across builds of the same list.
+void ensure_sorted() {
+  if (sorted_flag()) return;
+  for (int f = 0; f < ICPP_NUM_FAMILIES; ++f) {
+    std::stable_sort(table(f).begin(), table(f).end(), [](const Instance& a, const Instance& b) {
+      return strcmp(a.tile.name, b.tile.name) < 0;
+    });
+  }
+  sorted_flag() = true;
+}
+
+const Instance* lookup(int family, int inst) {
+  ensure_sorted();
+  if (family < 0 || family >= ICPP_NUM_FAMILIES) return nullptr;
+  if (inst < 0 || inst >= (int)table(family).size()) return nullptr;
+  return &table(family)[inst];
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+int esz_of(int dt) { return dt == DT_FP8 ? 1 : 2; }
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail((int)e, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return ICPP_OK;
+}
+
+hipError_t launch_splitk_reduce(int dt, const float* ws, void* C, const void* bias, int M, int N, int ldc,
+                                int splits, float alpha, int act, hipStream_t s) {
+  const size_t groups = (size_t)M * (N / 4);
+  const int blocks = (int)std::min<size_t>((groups + 255) / 256, 4096);
+  if (dt == DT_F16)
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act);
+  else if (dt == DT_BF16)
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_FP8>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act);
+  return hipGetLastError();
+}
+
+KArgs base_args() {
+  KArgs a;
+  memset(&a, 0, sizeof(a));
+  a.alpha = 1.f;
+  a.eps = 1e-5f;
+  return a;
+}
+
+}  // namespace
+
+int register_instance(const Instance& inst) {
+  if (inst.tile.family < 0 || inst.tile.family >= ICPP_NUM_FAMILIES) return -1;
+  table(inst.tile.family).push_back(inst);
+  sorted_flag() = false;
+  return (int)table(inst.tile.family).size();
+}
+
+}  // namespace icpp
+
+using namespace icpp;
+
+extern "C" {
+
+int icpp_abi_version(void) { return ICPP_ABI_VERSION; }
+
+const char* icpp_last_error(void) { return g_err.c_str(); }
+
+int icpp_num_instances(int family) {
+  ensure_sorted();
+  if (family < 0 || family >= ICPP_NUM_FAMILIES) return fail(ICPP_E_INSTANCE, "bad family %d", family);
+  return (int)table(family).size();
+}
+
+int icpp_instance_info(int family, int idx, icpp_tile_t* out) {
+  const Instance* in = lookup(family, idx);
+  if (!in) return fail(ICPP_E_INSTANCE, "no instance %d in family %d", idx, family);
+  if (!out) return fail(ICPP_E_ARG, "null output");
+  *out = in->tile;
+  return ICPP_OK;
+}
+
+size_t icpp_workspace_bytes(int family, int inst, int M, int N, int K, int split_k) {
+  (void)K;
+  const Instance* in = lookup(family, inst);
+  if (!in || M <= 0 || N <= 0) return 0;
+  if (family == ICPP_FAMILY_GEMM_LN_STATS) {
+    const size_t stat_cols = (size_t)ceil_div(N, in->wave_tile_n);
+    return (size_t)M * stat_cols * 2 * sizeof(float);
+  }
+  if ((family == ICPP_FAMILY_GEMM || family == ICPP_FAMILY_CONV2D) && split_k > 1)
+    return (size_t)split_k * M * N * sizeof(float);
+  return 0;
+}
+
+int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
+              int M, int N, int K, int lda, int ldb, int ldc, int act,
+              float scale_a, float scale_b, int split_k,
+              void* workspace, size_t ws_bytes, void* stream) {
+  const Instance* in = lookup(ICPP_FAMILY_GEMM, inst);
+  if (!in) return fail(ICPP_E_INSTANCE, "icpp_gemm: no GEMM instance %d", inst);
+  const icpp_tile_t& t = in->tile;
+  if (!A || !B || !C) return fail(ICPP_E_ARG, "icpp_gemm: null tensor");
+  if (M <= 0 || N <= 0 || K <= 0) return fail(ICPP_E_SHAPE, "icpp_gemm: empty shape M=%d N=%d K=%d", M, N, K);
+  if (act < ICPP_ACT_NONE || act > ICPP_ACT_SILU) return fail(ICPP_E_ARG, "icpp_gemm: bad act %d", act);
+  if (split_k < 1) return fail(ICPP_E_ARG, "icpp_gemm: split_k=%d", split_k);
+  const int e = esz_of(t.dtype);
+  const int vec = 16 / e;
+  if (N % 8 || lda % vec || ldb % vec || ldc % 8 || lda < K || ldb < N || ldc < N)
+    return fail(ICPP_E_SHAPE, "icpp_gemm: need N%%8==0, lda,ldb multiples of %d, ldc%%8==0 (N=%d lda=%d ldb=%d ldc=%d)",
+                vec, N, lda, ldb, ldc);
+  if (K % (t.block_k * split_k))
+    return fail(ICPP_E_SHAPE, "icpp_gemm: K=%d not a multiple of block_k*split_k=%d", K, t.block_k * split_k);
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias)))
+    return fail(ICPP_E_ARG, "icpp_gemm: pointers must be 16-byte aligned");
+  if ((uint64_t)t.block_m * lda * e > 0x7FFFFFFFull || (uint64_t)K * ldb * e > 0xFFFFFFF0ull)
+    return fail(ICPP_E_SHAPE, "icpp_gemm: operand exceeds the 4 GiB buffer range");
+  KArgs a = base_args();
+  a.A = A; a.B = B; a.bias = bias; a.C = C;
+  a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+  a.act = act; a.alpha = scale_a * scale_b;
+  a.k_split = K / split_k;
+  a.tiles_m = ceil_div(M, t.block_m);
+  a.tiles_n = ceil_div(N, t.block_n);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(a.tiles_m * a.tiles_n, split_k);
+  if (split_k > 1) {
+    const size_t need = (size_t)split_k * M * N * sizeof(float);
+    if (!workspace || ws_bytes < need || !aligned16(workspace))
+      return fail(ICPP_E_WORKSPACE, "icpp_gemm: split_k=%d needs %zu workspace bytes (got %zu)", split_k, need, ws_bytes);
+    if (ldc != N) return fail(ICPP_E_SHAPE, "icpp_gemm: split-K output needs ldc == N");
+    a.partial = 1;
+    a.ws = (float*)workspace;
+    int rc = check_launch(in->launch(a, grid, s), t.name);
+    if (rc) return rc;
+    return check_launch(launch_splitk_reduce(t.dtype, a.ws, C, bias, M, N, ldc, split_k, a.alpha, act, s), "splitk_reduce");
+  }
+  return check_launch(in->launch(a, grid, s), t.name);
+}
+
+int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
+                             const void* gamma, const void* beta, void* Y,
+                             int M, int N, int K, float eps,
+                             void* workspace, size_t ws_bytes, void* stream) {
+  if (family != ICPP_FAMILY_GEMM_LN_ROW && family != ICPP_FAMILY_GEMM_LN_STATS)
+    return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: family %d is not a LayerNorm family", family);
+  const Instance* in = lookup(family, inst);
+  if (!in) return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: no instance %d in family %d", inst, family);
+  const icpp_tile_t& t = in->tile;
+  if (!A || !B || !Y || !gamma || !beta) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: null tensor");
+  if (M <= 0 || N <= 0 || K <= 0) return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: empty shape");
+  if (N % 8 || K % 8) return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: need N%%8==0 and K%%8==0");
+  if (K % t.block_k) return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: K=%d not a multiple of block_k=%d", K, t.block_k);
+  if (!aligned16(A) || !aligned16(B) || !aligned16(Y) || !aligned16(gamma) || !aligned16(beta) || (bias && !aligned16(bias)))
+    return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: pointers must be 16-byte aligned");
+  if (!(eps > 0.f)) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: eps must be > 0");
+  KArgs a = base_args();
+  a.A = A; a.B = B; a.bias = bias; a.C = Y; a.gamma = gamma; a.beta = beta;
+  a.M = M; a.N = N; a.K = K; a.lda = K; a.ldb = N; a.ldc = N; a.eps = eps;
+  a.k_split = K;
+  a.tiles_m = ceil_div(M, t.block_m);
+  a.tiles_n = ceil_div(N, t.block_n);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(a.tiles_m * a.tiles_n, 1);
+  if (family == ICPP_FAMILY_GEMM_LN_ROW) {
+    if (a.tiles_n != 1) return fail(ICPP_E_SHAPE, "row LayerNorm instance %s needs N <= block_n (N=%d)", t.name, N);
+    return check_launch(in->launch(a, grid, s), t.name);
+  }
+  a.stat_cols = ceil_div(N, in->wave_tile_n);
+  const size_t need = (size_t)M * a.stat_cols * 2 * sizeof(float);
+  if (!workspace || ws_bytes < need || !aligned16(workspace))
+    return fail(ICPP_E_WORKSPACE, "icpp_gemm_bias_layernorm: needs %zu workspace bytes (got %zu)", need, ws_bytes);
+  a.ws = (float*)workspace;
+  int rc = check_launch(in->launch(a, grid, s), t.name);
+  if (rc) return rc;
+  hipLaunchKernelGGL(ln_finalize_kernel<DT_F16>, dim3(ceil_div(M, 4)), dim3(256), 0, s, Y, (const float*)a.ws, gamma, beta,
+                     M, N, N, a.stat_cols, in->wave_tile_n, eps);
+  return check_launch(hipGetLastError(), "ln_finalize");
+}
+
+int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
+                     int N, int H, int W, int C, int F, int KH, int KW,
+                     int stride, int pad, int dilation, int split_k,
+                     void* workspace, size_t ws_bytes, void* stream) {
+  const Instance* in = lookup(ICPP_FAMILY_CONV2D, inst);
+  if (!in) return fail(ICPP_E_INSTANCE, "icpp_conv2d_nhwc: no conv instance %d", inst);
+  const icpp_tile_t& t = in->tile;
+  if (!X || !Wt || !Y) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: null tensor");
+  if (N <= 0 || H <= 0 || W <= 0 || C <= 0 || F <= 0 || KH <= 0 || KW <= 0 || stride <= 0 || pad < 0 || dilation <= 0)
+    return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: bad geometry");
+  if (split_k < 1) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: split_k=%d", split_k);
+  const int OH = (H + 2 * pad - dilation * (KH - 1) - 1) / stride + 1;
+  const int OW = (W + 2 * pad - dilation * (KW - 1) - 1) / stride + 1;
+  if (OH <= 0 || OW <= 0) return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: empty output");
+  if (C % 8 || F % 8) return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: need C%%8==0 and F%%8==0 (C=%d F=%d)", C, F);
+  const long long Mg = (long long)N * OH * OW;
+  const long long Kg = (long long)KH * KW * C;
+  if (Mg > 0x7FFFFFFF || Kg % ((long long)t.block_k * split_k))
+    return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: K=%lld not a multiple of block_k*split_k=%d", Kg, t.block_k * split_k);
+  const unsigned long long xbytes = (unsigned long long)N * H * W * C * 2;
+  if (xbytes > 0xFFFFFFF0ull) return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: input exceeds the 4 GiB buffer range");
+  if (!aligned16(X) || !aligned16(Wt) || !aligned16(Y)) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: pointers must be 16-byte aligned");
+  KArgs a = base_args();
+  a.A = X; a.B = Wt; a.C = Y;
+  a.M = (int)Mg; a.N = F; a.K = (int)Kg; a.lda = 0; a.ldb = F; a.ldc = F;
+  a.k_split = (int)Kg / split_k;
+  a.tiles_m = ceil_div(a.M, t.block_m);
+  a.tiles_n = ceil_div(F, t.block_n);
+  a.cH = H; a.cW = W; a.cC = C; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH; a.cOW = OW;
+  a.a_bytes_total = (uint32_t)xbytes;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(a.tiles_m * a.tiles_n, split_k);
+  if (split_k > 1) {
+    const size_t need = (size_t)split_k * a.M * F * sizeof(float);
+    if (!workspace || ws_bytes < need || !aligned16(workspace))
+      return fail(ICPP_E_WORKSPACE, "icpp_conv2d_nhwc: split_k=%d needs %zu workspace bytes (got %zu)", split_k, need, ws_bytes);
+    a.partial = 1;
+    a.ws = (float*)workspace;
+    int rc = check_launch(in->launch(a, grid, s), t.name);
+    if (rc) return rc;
+    return check_launch(launch_splitk_reduce(DT_F16, a.ws, Y, nullptr, a.M, F, F, split_k, 1.f, ICPP_ACT_NONE, s), "splitk_reduce");
+  }
+  return check_launch(in->launch(a, grid, s), t.name);
+}
+
+}  // extern "C"

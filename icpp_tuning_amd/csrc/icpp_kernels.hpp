@@ -1,0 +1,697 @@
+// MFMA tile kernels for gfx950 (MI355X / CDNA4).
+//
+// One templated mainloop serves every fused op of the tuner:
+//   C[M,N] = epilogue( A[M,K] . B[K,N] )
+// A is row-major (K contiguous) -- either a dense matrix or an NHWC activation
+// gathered on the fly (implicit-GEMM conv); B is row-major (N contiguous), the
+// layout the reference hands its kernels (gemm.py:63-65, conv2d.py:223-233 with
+// the HWIO filter viewed as [KH*KW*C, F]).
+//
+// Data path per K tile (BK):
+//   global --(buffer_load_dwordx4, 16 B per lane, OOB lanes read 0)--> VGPR staging
+//   --> LDS (XOR-swizzled 16 B chunks, STAGES buffers)
+//   --> A fragments with ds_read_b128 (K contiguous per lane)
+//   --> B fragments with ds_read_b64_tr_b16 / ds_read_b64_tr_b8, which transpose
+//       the N-contiguous tile into the K-contiguous per-lane MFMA operand
+//   --> v_mfma (16x16x32 / 32x32x16 for f16/bf16, 16x16x128 / 32x32x64 f8f6f4).
+// The MFMA is issued with B as its first operand, so each lane ends up owning
+// one output row and 4 consecutive output columns: epilogues store 8-byte
+// (16-bit) or 16-byte (fp32) vectors and per-row reductions are lane shuffles.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace icpp {
+
+enum DType { DT_F16 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_F32 = 3 };
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3 };
+enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
+enum ALoad { A_DENSE = 0, A_IM2COL = 1 };
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+#define ICPP_LDS __attribute__((address_space(3)))
+#define ICPP_BUF_DWORD3 0x00020000  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+// Kernel arguments (passed by value; everything the launcher resolved on the host).
+struct KArgs {
+  const void* A;
+  const void* B;
+  const void* bias;   // [N] (f16 for f16, bf16 for bf16, f32 for fp8), or null
+  void* C;            // [M, ldc] output, or null when writing split-K partials
+  const void* gamma;  // LN [N]
+  const void* beta;   // LN [N]
+  float* ws;          // split-K partials [split][M][N] f32, or LN stats [M][stat_cols][2]
+  int M, N, K;
+  int lda, ldb, ldc;  // in elements
+  int act;
+  float alpha;        // scale_a * scale_b (fp8), 1 otherwise
+  float eps;
+  int k_split;        // K elements per split slice (multiple of BK)
+  int tiles_m, tiles_n;
+  int stat_cols;      // LN stats columns per row
+  int partial;        // 1: store fp32 partials to ws[blockIdx.y]
+  // implicit-GEMM conv geometry (A_IM2COL); GEMM M = Nb*OH*OW, K = KH*KW*C
+  int cH, cW, cC, cKW, cS, cP, cD, cOH, cOW;
+  uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
+};
+
+template <int DT> struct DTraits;
+template <> struct DTraits<DT_F16> { static constexpr int esz = 2; typedef _Float16 T; typedef _Float16 OutT; typedef _Float16 BiasT; };
+template <> struct DTraits<DT_BF16> { static constexpr int esz = 2; typedef __bf16 T; typedef __bf16 OutT; typedef __bf16 BiasT; };
+template <> struct DTraits<DT_FP8> { static constexpr int esz = 1; typedef uint8_t T; typedef __bf16 OutT; typedef float BiasT; };
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers. Lane layouts (verified on gfx950):
+//   16x16xK: operand lane l holds row/col (l%16), K slice (l/16)*EPL .. +EPL
+//            result lane l holds col (l%16), rows 4*(l/16)+0..3
+//   32x32xK: operand lane l holds row/col (l%32), K slice (l/32)*EPL .. +EPL
+//            result lane l holds col (l%32), rows 8*(j/4)+4*(l/32)+j%4, j<16
+// EPL (elements per lane) = 8 for 16-bit types, 32 for fp8.
+// ---------------------------------------------------------------------------
+template <int DT, int MF> struct Mfma;
+template <> struct Mfma<DT_F16, 16> {
+  static constexpr int KI = 32, FRAG_DW = 4, ACC = 4;
+  typedef i32x4 Frag; typedef f32x4 Acc;
+  static __device__ __forceinline__ Acc run(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<DT_F16, 32> {
+  static constexpr int KI = 16, FRAG_DW = 4, ACC = 16;
+  typedef i32x4 Frag; typedef f32x16 Acc;
+  static __device__ __forceinline__ Acc run(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<DT_BF16, 16> {
+  static constexpr int KI = 32, FRAG_DW = 4, ACC = 4;
+  typedef i32x4 Frag; typedef f32x4 Acc;
+  static __device__ __forceinline__ Acc run(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<DT_BF16, 32> {
+  static constexpr int KI = 16, FRAG_DW = 4, ACC = 16;
+  typedef i32x4 Frag; typedef f32x16 Acc;
+  static __device__ __forceinline__ Acc run(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+// fp8 = OCP e4m3fn on gfx950 (format code 0 for both operands, unit E8M0 scales = 127).
+template <> struct Mfma<DT_FP8, 16> {
+  static constexpr int KI = 128, FRAG_DW = 8, ACC = 4;
+  typedef i32x8 Frag; typedef f32x4 Acc;
+  static __device__ __forceinline__ Acc run(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+template <> struct Mfma<DT_FP8, 32> {
+  static constexpr int KI = 64, FRAG_DW = 8, ACC = 16;
+  typedef i32x8 Frag; typedef f32x16 Acc;
+  static __device__ __forceinline__ Acc run(Frag a, Frag b, Acc c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// small helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, ICPP_BUF_DWORD3);
+}
+__device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ void lds_store16(char ICPP_LDS* base, uint32_t off, i32x4 v) {
+  *reinterpret_cast<i32x4 ICPP_LDS*>(base + off) = v;
+}
+__device__ __forceinline__ i32x4 lds_load16(const char ICPP_LDS* base, uint32_t off) {
+  return *reinterpret_cast<const i32x4 ICPP_LDS*>(base + off);
+}
+__device__ __forceinline__ i32x2 lds_tr16(const char ICPP_LDS* base, uint32_t off) {
+  i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 ICPP_LDS*)(base + off));
+  return __builtin_bit_cast(i32x2, v);
+}
+__device__ __forceinline__ i32x2 lds_tr8(const char ICPP_LDS* base, uint32_t off) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((i32x2 ICPP_LDS*)(base + off));
+}
+
+// Epilogue activation, branch-free so the unrolled epilogue stays small enough
+// for the accumulators to remain in registers:
+//   GELU-tanh(x) = 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
+//   SiLU(x)      = x * sigmoid(x)
+__device__ __forceinline__ float apply_act(float x, int act) {
+  const float u2 = 1.5957691216057308f * (x + 0.044715f * x * x * x);
+  const float z = (act == ACT_GELU_TANH) ? u2 : x;
+  const float sg = 1.f / (1.f + __expf(-z));
+  const float r = (act >= ACT_GELU_TANH) ? x * sg : x;
+  return (act == ACT_RELU) ? fmaxf(x, 0.f) : r;
+}
+
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
+
+template <typename T> struct Vec4Store;
+template <> struct Vec4Store<_Float16> {
+  static __device__ __forceinline__ void st(void* p, f32x4 v) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    *reinterpret_cast<h4*>(p) = h;
+  }
+  static __device__ __forceinline__ f32x4 ld(const void* p) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 h = *reinterpret_cast<const h4*>(p);
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  }
+};
+template <> struct Vec4Store<__bf16> {
+  static __device__ __forceinline__ void st(void* p, f32x4 v) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    b4 h = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+    *reinterpret_cast<b4*>(p) = h;
+  }
+  static __device__ __forceinline__ f32x4 ld(const void* p) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    b4 h = *reinterpret_cast<const b4*>(p);
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  }
+};
+template <> struct Vec4Store<float> {
+  static __device__ __forceinline__ void st(void* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+  static __device__ __forceinline__ f32x4 ld(const void* p) { return *reinterpret_cast<const f32x4*>(p); }
+};
+
+// ---------------------------------------------------------------------------
+// Tile geometry
+// ---------------------------------------------------------------------------
+template <int DT, int BM_, int BN_, int BK_, int WM_, int WN_, int MF_, int STAGES_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, MF = MF_, STAGES = STAGES_;
+  static constexpr int ESZ = DTraits<DT>::esz;
+  static constexpr int THREADS = WM * WN * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  static constexpr int TM = WTM / MF, TN = WTN / MF;  // MFMA tiles per wave
+  typedef Mfma<DT, MF> Op;
+  static constexpr int KI = Op::KI;
+  static constexpr int CH = 16 / ESZ;                 // elements per 16-byte chunk
+  static constexpr int ROWB_A = BK * ESZ;             // LDS bytes per A row
+  static constexpr int ROWB_B = BN * ESZ;             // LDS bytes per B row
+  static constexpr int CPR_A = ROWB_A / 16, CPR_B = ROWB_B / 16;
+  static constexpr int A_CHUNKS = BM * CPR_A, B_CHUNKS = BK * CPR_B;
+  static constexpr int SA = (A_CHUNKS + THREADS - 1) / THREADS;  // chunks per thread
+  static constexpr int SB = (B_CHUNKS + THREADS - 1) / THREADS;
+  static constexpr bool A_EVEN = (A_CHUNKS % THREADS) == 0, B_EVEN = (B_CHUNKS % THREADS) == 0;
+  static constexpr int A_BYTES = BM * ROWB_A, B_BYTES = BK * ROWB_B;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int LDS_BYTES = STAGE_BYTES * STAGES;
+  static constexpr int RPB_A = (ROWB_A >= 128) ? 1 : (128 / ROWB_A);
+  static constexpr int SWZ_A = (CPR_A < 8) ? CPR_A : 8;
+
+  static_assert(WTM % MF == 0 && WTN % MF == 0, "wave tile must be a multiple of the MFMA tile");
+  static_assert(BK % KI == 0, "BK must be a multiple of the MFMA K");
+  static_assert(CPR_B >= 8, "B rows must span >= 8 chunks (128 B) for the transpose-read swizzle");
+  static_assert(CPR_A >= 2, "A rows must span >= 2 chunks");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS overflow");
+
+  // A: row r, logical 16 B chunk c -> byte offset in the A region
+  static __device__ __forceinline__ uint32_t a_off(int r, int c) {
+    return (uint32_t)(r * ROWB_A + ((c ^ ((r / RPB_A) % SWZ_A)) << 4));
+  }
+  // B: row k, logical chunk c -> byte offset in the B region. The XOR keeps the
+  // rows that one transpose read touches together in distinct bank groups
+  // (4 rows x 32 B for b16, 8 rows x 16 B for b8).
+  static __device__ __forceinline__ uint32_t b_off(int k, int c) {
+    const int s = (ESZ == 2) ? ((k & 3) << 1) : (k & 7);
+    return (uint32_t)(k * ROWB_B + ((c ^ s) << 4));
+  }
+};
+
+// ---------------------------------------------------------------------------
+// The mainloop + epilogue kernel
+// ---------------------------------------------------------------------------
+template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int STAGES, int EPI, int ALOAD>
+__global__ void __launch_bounds__(WM * WN * 64)
+gemm_kernel(KArgs p) {
+  typedef Tile<DT, BM, BN, BK, WM, WN, MF, STAGES> G;
+  typedef typename G::Op Op;
+  typedef typename Op::Frag Frag;
+  typedef typename Op::Acc Acc;
+  typedef typename DTraits<DT>::OutT OutT;
+  typedef typename DTraits<DT>::BiasT BiasT;
+  constexpr int ESZ = G::ESZ;
+
+  __shared__ __attribute__((aligned(16))) char smem_raw[G::LDS_BYTES];
+  char ICPP_LDS* smem = (char ICPP_LDS*)smem_raw;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // ---- tile index: XCD-contiguous ranges of the grid, then grouped-M order ----
+  int t = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) t = (t & 7) * (nb >> 3) + (t >> 3);
+  const int GROUP = 8;
+  const int group_size = GROUP * p.tiles_n;
+  const int group = t / group_size;
+  const int first_m = group * GROUP;
+  const int gm = min(p.tiles_m - first_m, GROUP);
+  const int tile_m = first_m + (t % group_size) % gm;
+  const int tile_n = (t % group_size) / gm;
+  const int row0 = tile_m * BM, col0 = tile_n * BN;
+
+  const int kz = blockIdx.y;
+  const int k_begin = kz * p.k_split;
+  const int k_len = min(p.k_split, p.K - k_begin);
+  const int nk = k_len / BK;
+
+  // ---- global sources (raw buffer resources; out-of-range lanes read zeros) ----
+  const char* Ab = (const char*)p.A;
+  const char* Bb = (const char*)p.B;
+  __amdgpu_buffer_rsrc_t ra, rb;
+  uint32_t a_row_off[G::SA];
+  int a_chunk[G::SA];
+  // conv gather state
+  int a_img[ALOAD == A_IM2COL ? G::SA : 1], a_ih0[ALOAD == A_IM2COL ? G::SA : 1], a_iw0[ALOAD == A_IM2COL ? G::SA : 1];
+  if constexpr (ALOAD == A_DENSE) {
+    const uint64_t rem = (uint64_t)(p.M > row0 ? p.M - row0 : 0) * (uint64_t)p.lda * ESZ;
+    ra = make_rsrc(Ab + (size_t)row0 * p.lda * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
+#pragma unroll
+    for (int i = 0; i < G::SA; ++i) {
+      const int q = tid + i * G::THREADS;
+      const int r = q / G::CPR_A;
+      a_chunk[i] = q % G::CPR_A;
+      a_row_off[i] = (uint32_t)(r * p.lda * ESZ + k_begin * ESZ + a_chunk[i] * 16);
+    }
+  } else {
+    ra = make_rsrc(Ab, (uint32_t)p.a_bytes_total);
+#pragma unroll
+    for (int i = 0; i < G::SA; ++i) {
+      const int q = tid + i * G::THREADS;
+      const int r = q / G::CPR_A;
+      a_chunk[i] = q % G::CPR_A;
+      const int m = row0 + r;
+      const int ohw = p.cOH * p.cOW;
+      const int img = m / ohw;
+      const int rem = m - img * ohw;
+      const int oh = rem / p.cOW, ow = rem - (rem / p.cOW) * p.cOW;
+      a_img[i] = (m < p.M) ? img : -1;
+      a_ih0[i] = oh * p.cS - p.cP;
+      a_iw0[i] = ow * p.cS - p.cP;
+      a_row_off[i] = 0;
+    }
+  }
+  {
+    const uint64_t rem = ((uint64_t)(p.K - 1) * p.ldb + (uint64_t)(p.N - col0)) * ESZ;
+    rb = make_rsrc(Bb + (size_t)col0 * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
+  }
+  uint32_t b_off_g[G::SB];
+#pragma unroll
+  for (int i = 0; i < G::SB; ++i) {
+    const int q = tid + i * G::THREADS;
+    const int k = q / G::CPR_B, c = q % G::CPR_B;
+    b_off_g[i] = (uint32_t)((k_begin + k) * p.ldb * ESZ + c * 16);
+  }
+
+  i32x4 ra_st[G::SA], rb_st[G::SB];
+
+  auto load_tile = [&](int kt) {
+    if constexpr (ALOAD == A_DENSE) {
+#pragma unroll
+      for (int i = 0; i < G::SA; ++i)
+        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) ra_st[i] = buf_load16(ra, a_row_off[i] + (uint32_t)(kt * BK * ESZ));
+    } else {
+      // K index of this chunk -> (kh, kw, c); one filter tap per chunk since C % 8 == 0
+      const int kbase = k_begin + kt * BK;
+#pragma unroll
+      for (int i = 0; i < G::SA; ++i) {
+        const int k = kbase + a_chunk[i] * G::CH;
+        const int tap = k / p.cC;
+        const int ci = k - tap * p.cC;
+        const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
+        const int ih = a_ih0[i] + kh * p.cD, iw = a_iw0[i] + kw * p.cD;
+        const bool ok = a_img[i] >= 0 && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW && k < p.K;
+        const uint32_t off = ok ? (uint32_t)((((a_img[i] * p.cH + ih) * p.cW + iw) * p.cC + ci) * ESZ)
+                                : (uint32_t)p.a_bytes_total;
+        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) ra_st[i] = buf_load16(ra, off);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < G::SB; ++i)
+      if (G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS) rb_st[i] = buf_load16(rb, b_off_g[i] + (uint32_t)(kt * BK * p.ldb * ESZ));
+  };
+  auto store_tile = [&](int s) {
+    char ICPP_LDS* as = smem + s * G::STAGE_BYTES;
+    char ICPP_LDS* bs = as + G::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < G::SA; ++i) {
+      const int q = tid + i * G::THREADS;
+      if (G::A_EVEN || q < G::A_CHUNKS) lds_store16(as, G::a_off(q / G::CPR_A, q % G::CPR_A), ra_st[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < G::SB; ++i) {
+      const int q = tid + i * G::THREADS;
+      if (G::B_EVEN || q < G::B_CHUNKS) lds_store16(bs, G::b_off(q / G::CPR_B, q % G::CPR_B), rb_st[i]);
+    }
+  };
+
+  Acc acc[G::TM][G::TN];
+#pragma unroll
+  for (int i = 0; i < G::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < G::TN; ++j) acc[i][j] = Acc{};
+
+  // per-lane fragment addressing (constant over the K loop)
+  const int a_lrow = wm * G::WTM + (lane % MF);
+  const int a_kgrp = lane / MF;                            // 0..3 (MF16) / 0..1 (MF32)
+  // B transpose-read lane mapping (group of 16 lanes reads 4 rows x 16 cols (b16) or 8 rows x 16 cols (b8))
+  const int li = lane & 15;
+  const int b_ncol_base = wn * G::WTN + ((MF == 32) ? 16 * ((lane >> 4) & 1) : 0);
+  const int b_kgrp = (MF == 32) ? (lane >> 5) : (lane >> 4);
+
+  auto compute = [&](int s) {
+    const char ICPP_LDS* as = smem + s * G::STAGE_BYTES;
+    const char ICPP_LDS* bs = as + G::A_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < BK / G::KI; ++ks) {
+      Frag af[G::TM], bf[G::TN];
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        const int r = a_lrow + tm * MF;
+        if constexpr (ESZ == 2) {
+          const int c = (ks * G::KI) / 8 + a_kgrp;
+          af[tm] = lds_load16(as, G::a_off(r, c));
+        } else {
+          const int c = (ks * G::KI) / 16 + a_kgrp * 2;
+          i32x4 lo = lds_load16(as, G::a_off(r, c));
+          i32x4 hi = lds_load16(as, G::a_off(r, c + 1));
+          af[tm] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+#pragma unroll
+      for (int tn = 0; tn < G::TN; ++tn) {
+        const int n0 = b_ncol_base + tn * MF;
+        if constexpr (ESZ == 2) {
+          const int kb = ks * G::KI + b_kgrp * 8;
+          const int col = n0 + 4 * (li & 3);
+          const int c = col >> 3, within = (col & 7) * 2;
+          const int r0 = kb + (li >> 2), r1 = kb + 4 + (li >> 2);
+          i32x2 lo = lds_tr16(bs, G::b_off(r0, c) + within);
+          i32x2 hi = lds_tr16(bs, G::b_off(r1, c) + within);
+          bf[tn] = i32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          const int kb = ks * G::KI + b_kgrp * 32;
+          const int col = n0 + 8 * (li & 1);
+          const int c = col >> 4, within = col & 15;
+          i32x2 v[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) v[rr] = lds_tr8(bs, G::b_off(kb + 8 * rr + (li >> 1), c) + within);
+          bf[tn] = i32x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
+        }
+      }
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn) acc[tm][tn] = Op::run(bf[tn], af[tm], acc[tm][tn]);
+    }
+  };
+
+  // ---- pipelined mainloop ----
+  if (nk > 0) {
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int it = 0; it < nk; ++it) {
+      const int cur = (STAGES == 2) ? (it & 1) : 0;
+      if (it + 1 < nk) load_tile(it + 1);
+      compute(cur);
+      if (it + 1 < nk) {
+        if constexpr (STAGES == 1) __syncthreads();
+        store_tile((STAGES == 2) ? (cur ^ 1) : 0);
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- epilogue ----
+  // lane owns output row (lane % MF) of each MFMA tile and groups of 4 consecutive columns
+  constexpr int NG = Op::ACC / 4;  // column groups per MFMA tile
+  auto out_row = [&](int tm) { return row0 + wm * G::WTM + tm * MF + (lane % MF); };
+  auto out_col = [&](int tn, int g) {
+    return col0 + wn * G::WTN + tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
+  };
+  auto get4 = [&](int tm, int tn, int g) {
+    return f32x4{acc[tm][tn][4 * g + 0], acc[tm][tn][4 * g + 1], acc[tm][tn][4 * g + 2], acc[tm][tn][4 * g + 3]};
+  };
+
+  if constexpr (EPI == EPI_STORE) {
+    if (p.partial) {
+      float* ws = p.ws + (size_t)kz * p.M * p.N;
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        const int m = out_row(tm);
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const int n = out_col(tn, g);
+            if (m < p.M && n < p.N) Vec4Store<float>::st(ws + (size_t)m * p.N + n, get4(tm, tn, g));
+          }
+      }
+    } else {
+      OutT* C = (OutT*)p.C;
+      const BiasT* bias = (const BiasT*)p.bias;
+#pragma unroll
+      for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int n = out_col(tn, g);
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (bias != nullptr && n < p.N) bv = Vec4Store<BiasT>::ld(bias + n);
+#pragma unroll
+          for (int tm = 0; tm < G::TM; ++tm) {
+            const int m = out_row(tm);
+            f32x4 v = get4(tm, tn, g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e] * p.alpha + bv[e], p.act);
+            if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
+          }
+        }
+    }
+  } else {
+    // LayerNorm epilogues: x = acc + bias, statistics over valid columns (n < N)
+    OutT* C = (OutT*)p.C;
+    const BiasT* bias = (const BiasT*)p.bias;
+    float xs[G::TM][G::TN][Op::ACC];
+#pragma unroll
+    for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const int n = out_col(tn, g);
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if (bias != nullptr && n < p.N) bv = Vec4Store<BiasT>::ld(bias + n);
+        const bool ok = n < p.N;
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] = ok ? (acc[tm][tn][4 * g + e] + bv[e]) : 0.f;
+      }
+    // row sums over this wave's columns, reduced across the lanes sharing a row
+    auto lane_reduce = [&](float v) {
+      if (MF == 16) {
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+      } else {
+        v += __shfl_xor(v, 32);
+      }
+      return v;
+    };
+    const int wcol0 = col0 + wn * G::WTN;
+    const int wcnt = max(0, min(G::WTN, p.N - wcol0));
+    if constexpr (EPI == EPI_LN_STATS) {
+      float* ws = p.ws;
+      const int scol = wcol0 / G::WTN;
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        float s = 0.f;
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int e = 0; e < Op::ACC; ++e) s += xs[tm][tn][e];
+        s = lane_reduce(s);
+        const float mean = wcnt > 0 ? s / (float)wcnt : 0.f;
+        float q = 0.f;
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const bool ok = out_col(tn, g) < p.N;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float d = xs[tm][tn][4 * g + e] - mean;
+              q += ok ? d * d : 0.f;
+            }
+          }
+        q = lane_reduce(q);
+        const int m = out_row(tm);
+        if (lane < MF && m < p.M && scol < p.stat_cols) {
+          ws[((size_t)m * p.stat_cols + scol) * 2 + 0] = mean;
+          ws[((size_t)m * p.stat_cols + scol) * 2 + 1] = q;
+        }
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const int n = out_col(tn, g);
+            f32x4 v = {xs[tm][tn][4 * g], xs[tm][tn][4 * g + 1], xs[tm][tn][4 * g + 2], xs[tm][tn][4 * g + 3]};
+            if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
+          }
+      }
+    } else {
+      // EPI_LN_ROW: the workgroup owns whole rows (tiles_n == 1, N <= BN); two-pass
+      // mean / centred variance in registers, cross-wave through LDS.
+      __syncthreads();  // mainloop LDS no longer needed
+      float ICPP_LDS* red = (float ICPP_LDS*)smem;       // [WN][BM]
+      float ICPP_LDS* red2 = red + WN * BM;               // [WN][BM]
+      const BiasT* gamma = (const BiasT*)p.gamma;
+      const BiasT* beta = (const BiasT*)p.beta;
+      const float inv_n = 1.f / (float)p.N;
+      float mean[G::TM], rstd[G::TM];
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        float s = 0.f;
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int e = 0; e < Op::ACC; ++e) s += xs[tm][tn][e];
+        s = lane_reduce(s);
+        if (lane < MF) red[wn * BM + wm * G::WTM + tm * MF + lane] = s;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        float s = 0.f;
+        const int lr = wm * G::WTM + tm * MF + (lane % MF);
+#pragma unroll
+        for (int w = 0; w < WN; ++w) s += red[w * BM + lr];
+        mean[tm] = s * inv_n;
+        float q = 0.f;
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const bool ok = out_col(tn, g) < p.N;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float d = xs[tm][tn][4 * g + e] - mean[tm];
+              q += ok ? d * d : 0.f;
+            }
+          }
+        q = lane_reduce(q);
+        if (lane < MF) red2[wn * BM + lr] = q;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        float q = 0.f;
+        const int lr = wm * G::WTM + tm * MF + (lane % MF);
+#pragma unroll
+        for (int w = 0; w < WN; ++w) q += red2[w * BM + lr];
+        rstd[tm] = rsqrtf(q * inv_n + p.eps);
+      }
+#pragma unroll
+      for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int n = out_col(tn, g);
+          if (n >= p.N) continue;
+          const f32x4 gv = Vec4Store<BiasT>::ld(gamma + n);
+          const f32x4 bv = Vec4Store<BiasT>::ld(beta + n);
+#pragma unroll
+          for (int tm = 0; tm < G::TM; ++tm) {
+            const int m = out_row(tm);
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (xs[tm][tn][4 * g + e] - mean[tm]) * rstd[tm] * gv[e] + bv[e];
+            if (m < p.M) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
+          }
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K reduction + epilogue: C = act(alpha * sum_z ws[z] + bias)
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(256)
+splitk_reduce_kernel(const float* __restrict__ ws, void* C, const void* bias, int M, int N, int ldc,
+                     int splits, float alpha, int act) {
+  typedef typename DTraits<DT>::OutT OutT;
+  typedef typename DTraits<DT>::BiasT BiasT;
+  const size_t groups = (size_t)M * (N / 4);
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < groups; gi += stride) {
+    const int m = (int)(gi / (N / 4));
+    const int n = (int)(gi % (N / 4)) * 4;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int z = 0; z < splits; ++z) s += Vec4Store<float>::ld(ws + ((size_t)z * M + m) * N + n);
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr) bv = Vec4Store<BiasT>::ld((const BiasT*)bias + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] = apply_act(s[e] * alpha + bv[e], act);
+    Vec4Store<OutT>::st((OutT*)C + (size_t)m * ldc + n, s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Two-pass LayerNorm finalize: combine per-(row, column block) (mean, M2)
+// partials (Chan et al. pairwise update), then normalise the row in place.
+// One wave per row; 4 rows per 256-thread workgroup.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(256)
+ln_finalize_kernel(void* C, const float* __restrict__ stats, const void* gamma, const void* beta,
+                   int M, int N, int ldc, int stat_cols, int block_cols, float eps) {
+  typedef typename DTraits<DT>::OutT OutT;
+  typedef typename DTraits<DT>::BiasT BiasT;
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  // every lane combines all partials (stat_cols is small) so no broadcast is needed
+  float n_acc = 0.f, mean = 0.f, m2 = 0.f;
+  for (int j = 0; j < stat_cols; ++j) {
+    const float nb = (float)max(0, min(block_cols, N - j * block_cols));
+    if (nb <= 0.f) continue;
+    const float mb = stats[((size_t)m * stat_cols + j) * 2 + 0];
+    const float qb = stats[((size_t)m * stat_cols + j) * 2 + 1];
+    const float nt = n_acc + nb;
+    const float d = mb - mean;
+    mean += d * (nb / nt);
+    m2 += qb + d * d * (n_acc * nb / nt);
+    n_acc = nt;
+  }
+  const float rstd = rsqrtf(m2 / (float)N + eps);
+  OutT* row = (OutT*)C + (size_t)m * ldc;
+  const BiasT* g = (const BiasT*)gamma;
+  const BiasT* b = (const BiasT*)beta;
+  for (int n = lane * 4; n < N; n += 256) {
+    f32x4 x = Vec4Store<OutT>::ld(row + n);
+    const f32x4 gv = Vec4Store<BiasT>::ld(g + n);
+    const f32x4 bv = Vec4Store<BiasT>::ld(b + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = (x[e] - mean) * rstd * gv[e] + bv[e];
+    Vec4Store<OutT>::st(row + n, x);
+  }
+}
+
+}  // namespace icpp

@@ -1,0 +1,61 @@
+// Instance registry shared by the generated instance translation units and the
+// C ABI.  Each AOT-compiled tile configuration registers one Instance from a
+// static initializer when the shared library is loaded.
+#pragma once
+#include "icpp_kernels.hpp"
+#include "../../include/icpp_hip.h"
+
+namespace icpp {
+
+typedef hipError_t (*LaunchFn)(const KArgs&, dim3, hipStream_t);
+
+struct Instance {
+  icpp_tile_t tile;
+  int epi;
+  int aload;
+  int wave_tile_n;
+  LaunchFn launch;
+};
+
+int register_instance(const Instance& inst);
+
+template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int ST, int EPI, int AL>
+hipError_t launch_instance(const KArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_kernel<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>), grid, dim3(WM * WN * 64), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int ST, int EPI, int AL>
+Instance make_instance(int family, const char* name) {
+  typedef Tile<DT, BM, BN, BK, WM, WN, MF, ST> G;
+  Instance in{};
+  in.tile.family = family;
+  in.tile.dtype = DT;
+  in.tile.block_m = BM;
+  in.tile.block_n = BN;
+  in.tile.block_k = BK;
+  in.tile.waves_m = WM;
+  in.tile.waves_n = WN;
+  in.tile.stages = ST;
+  in.tile.mfma_m = MF;
+  in.tile.mfma_n = MF;
+  in.tile.mfma_k = Mfma<DT, MF>::KI;
+  in.tile.lds_bytes = G::LDS_BYTES;
+  in.tile.threads = G::THREADS;
+  int i = 0;
+  for (; name[i] && i < (int)sizeof(in.tile.name) - 1; ++i) in.tile.name[i] = name[i];
+  in.tile.name[i] = 0;
+  in.epi = EPI;
+  in.aload = AL;
+  in.wave_tile_n = G::WTN;
+  in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>;
+  return in;
+}
+
+}  // namespace icpp
+
+#define ICPP_CAT2(a, b) a##b
+#define ICPP_CAT(a, b) ICPP_CAT2(a, b)
+#define ICPP_INSTANCE(FAM, DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL, NAME)                                   \
+  static const int ICPP_CAT(icpp_reg_, __LINE__) = icpp::register_instance(                                  \
+      icpp::make_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>(FAM, NAME));

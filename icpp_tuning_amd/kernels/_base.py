@@ -1,0 +1,125 @@
+"""Descriptor base for the AOT-compiled gfx950 instances.
+
+A raw config is the reference's dict layout (``block_M, block_N, block_K,
+num_stages, thread_num`` [+ ``split_k``], gemm.py:40-47) plus the gfx950
+template parameters ``waves_m, waves_n, mfma``.  Each raw config maps to
+exactly one compiled instance of libicpp_hip.so (plus a split-K factor), so
+"compile" is an index lookup.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, List, Optional, Sequence
+
+from ..autotuner.cost_model import TuneConfig
+from ..autotuner.gpu_spec import GPUSpec
+from ..autotuner.interface import TileLangKernelBase
+from ..autotuner.search_space import prune_for_shape
+from ..instances import ESZ, FAMILY_ID, INSTANCES, MFMA_K, Inst
+
+
+def family_instances(family: str) -> List[Inst]:
+    """Instances of a family in library index order (the ABI sorts by name)."""
+    return sorted((i for i in INSTANCES if i.family == family), key=lambda i: i.name)
+
+
+def raw_from_inst(inst: Inst, split_k: Optional[int] = None) -> Dict[str, Any]:
+    raw = {
+        "block_M": inst.bm, "block_N": inst.bn, "block_K": inst.bk,
+        "num_stages": inst.stages, "thread_num": inst.threads,
+        "waves_m": inst.wm, "waves_n": inst.wn,
+        "mfma": f"{inst.mf}x{inst.mf}x{MFMA_K[(inst.dtype, inst.mf)]}",
+    }
+    if split_k is not None:
+        raw["split_k"] = split_k
+    return raw
+
+
+class InstanceDescriptor(TileLangKernelBase):
+    """Descriptor whose candidate space is the compiled instance set of one family/dtype."""
+
+    family: str = "gemm"
+    dtype: str = "f16"
+    split_k_values: Sequence[int] = (1,)
+
+    def __init__(self, dtype: Optional[str] = None):
+        if dtype is not None:
+            self.dtype = dtype
+
+    # ---- instance mapping --------------------------------------------------
+    def instances(self) -> List[Inst]:
+        return [i for i in family_instances(self.family) if i.dtype == self.dtype]
+
+    def instance_index(self, raw: Dict[str, Any]) -> int:
+        mf = int(str(raw["mfma"]).split("x")[0]) if "mfma" in raw else None
+        for idx, inst in enumerate(family_instances(self.family)):
+            if inst.dtype != self.dtype:
+                continue
+            if (inst.bm, inst.bn, inst.bk, inst.stages, inst.threads) != (
+                    raw["block_M"], raw["block_N"], raw["block_K"], raw["num_stages"], raw["thread_num"]):
+                continue
+            if "waves_m" in raw and (inst.wm, inst.wn) != (raw["waves_m"], raw["waves_n"]):
+                continue
+            if mf is not None and inst.mf != mf:
+                continue
+            return idx
+        raise KeyError(f"{self.name}: no compiled {self.family}/{self.dtype} instance for {self.format_config(raw)}")
+
+    def instance_of(self, raw: Dict[str, Any]) -> Inst:
+        return family_instances(self.family)[self.instance_index(raw)]
+
+    # ---- descriptor API ----------------------------------------------------
+    def k_extent(self, **shape) -> int:
+        return shape["K"]
+
+    def shape_ok(self, inst: Inst, split_k: int, **shape) -> bool:
+        return self.k_extent(**shape) % (inst.bk * split_k) == 0
+
+    def get_raw_configs(self, **shape_kwargs: Any) -> List[Dict[str, Any]]:
+        out = []
+        for inst in self.instances():
+            for sk in self.split_k_values:
+                if self.shape_ok(inst, sk, **shape_kwargs):
+                    out.append(raw_from_inst(inst, sk if len(self.split_k_values) > 1 or sk != 1 else None))
+        return out
+
+    def raw_config_to_tune_config(self, raw: Dict[str, Any]) -> TuneConfig:
+        e = ESZ[self.dtype]
+        try:
+            vgprs = instance_vgprs(self.instance_of(raw))
+        except KeyError:
+            vgprs = 0
+        return TuneConfig(
+            block_M=raw["block_M"], block_N=raw["block_N"], block_K=raw["block_K"],
+            num_stages=raw["num_stages"], num_warps=raw["thread_num"] // 64, warp_size=64,
+            a_bytes=e, b_bytes=e, mfma=raw.get("mfma", ""), waves_m=raw.get("waves_m", 0),
+            waves_n=raw.get("waves_n", 0), split_k=raw.get("split_k", 1), vgprs=vgprs)
+
+    def gemm_mn(self, **shape) -> tuple:
+        return shape["M"], shape["N"]
+
+    def prune(self, raw_configs: List[Dict[str, Any]], hw: GPUSpec, **shape_kwargs: Any) -> List[Dict[str, Any]]:
+        """CDNA4 L1-L4 pruning (LDS, VGPR, occupancy, CU fill) on the compiled set."""
+        if not hw.has_mfma_model:
+            return raw_configs
+        M, N = self.gemm_mn(**shape_kwargs)
+        cfgs = [self.raw_config_to_tune_config(r) for r in raw_configs]
+        keep = set(id(c) for c in prune_for_shape(cfgs, hw, M, N))
+        return [r for r, c in zip(raw_configs, cfgs) if id(c) in keep]
+
+
+__all__ = ["InstanceDescriptor", "family_instances", "raw_from_inst"]
+
+
+def compiled_resources(inst: Inst) -> Dict[str, int]:
+    """Compiler-reported registers of an instance (empty when the library is not built)."""
+    from .._lib import resources
+
+    return resources().get(inst.name, {})
+
+
+def instance_vgprs(inst: Inst) -> int:
+    r = compiled_resources(inst)
+    if not r:
+        return 0
+    return -(-(r.get("vgprs", 0)) // 8) * 8 + r.get("agprs", 0)

@@ -1,0 +1,80 @@
+"""fp8 (OCP e4m3fn) GEMM + bias + SiLU with per-tensor scales, bf16 out.
+
+No reference kernel exists for this op; it follows the GEMM+bias+act module's
+API (gemm_bias_act.py) with the quantised-inference contract of the benchmark:
+``kernel(a_q, b_q, scale_a, scale_b, bias) -> act(scale_a*scale_b * a_q @ b_q + bias)``
+with fp32 bias and fp32 accumulation; scales are applied once in the epilogue.
+Small M is HBM-bound, so split-K candidates put >= 256 workgroups on B.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..autotuner.cost_model import ACT_PRIMITIVE, make_matmul_spec
+from ..autotuner.gpu_spec import get_gpu_spec
+from ..autotuner.interface import select_best
+from .. import inputs as _inputs
+from ._base import InstanceDescriptor
+from .gemm import CompiledGemm
+
+
+class Fp8GemmBiasActDescriptor(InstanceDescriptor):
+    family = "gemm"
+    dtype = "fp8"
+    split_k_values = (1, 2, 4, 8)
+
+    def __init__(self, act: str = "silu"):
+        super().__init__("fp8")
+        self.act = act
+
+    @property
+    def name(self) -> str:
+        return f"fp8_gemm_bias_{self.act}"
+
+    def make_op_spec(self, raw_config=None, M=0, N=0, K=0, **kw):
+        sk = raw_config.get("split_k", 1) if raw_config else 1
+        return make_matmul_spec(M=M, N=N, K=K // sk, primitives=["bias_add", ACT_PRIMITIVE[self.act]],
+                                dtype="fp8", output_element_bytes=2)
+
+    def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
+        sk = raw.get("split_k", 1)
+        if sk <= 1:
+            return base_score
+        hw = get_gpu_spec()
+        t_main = max(2.0 * M * N * K / (hw.peak_tflops("fp8") * 1e12),
+                     (M * K + K * N) / (hw.mem_bandwidth_gbps * 1e9))
+        t_red = (2.0 * sk * M * N * 4 + M * N * 2) / (hw.mem_bandwidth_gbps * 1e9) + 4e-6
+        return base_score * t_main / (t_main + t_red)
+
+    def make_inputs(self, M, N, K, **kw):
+        d = _inputs.config5(M, N, K, device="cuda")
+        d["C"] = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        return d
+
+    def make_runner(self, raw, inputs, M, N, K, **kw):
+        k = CompiledGemm(self, M, N, K, raw, act=self.act)
+        return lambda: k(inputs["A"], inputs["B"], inputs["bias"], out=inputs["C"],
+                         scale_a=inputs["scale_a"], scale_b=inputs["scale_b"])
+
+
+DESCRIPTOR = Fp8GemmBiasActDescriptor("silu")
+
+
+def get_configs(M, K, N: int = 0):
+    return DESCRIPTOR.get_raw_configs(M=M, N=N, K=K)
+
+
+class CompiledFp8Gemm(CompiledGemm):
+    def __call__(self, a_q, b_q, scale_a, scale_b, bias=None, out=None):
+        return super().__call__(a_q, b_q, bias=bias, out=out, scale_a=float(scale_a), scale_b=float(scale_b))
+
+
+def build_kernel(M, N, K, config=None, act: str = "silu"):
+    d = DESCRIPTOR if act == "silu" else Fp8GemmBiasActDescriptor(act)
+    if config is None:
+        config, _ = select_best(d, M=M, N=N, K=K)
+    return CompiledFp8Gemm(d, M, N, K, config, act=act)
+
+
+__all__ = ["DESCRIPTOR", "Fp8GemmBiasActDescriptor", "build_kernel", "get_configs"]

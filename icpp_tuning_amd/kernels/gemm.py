@@ -1,0 +1,103 @@
+"""Plain GEMM C = A @ B (fp16 in, fp32 accumulate, fp16 out).
+
+Mirrors kernel/tilelang/gemm/gemm.py: ``get_configs`` (:24-48), ``build_kernel``
+(:84-89, out-allocating ``kernel(a, b) -> C``) and ``DESCRIPTOR`` (:97-114,
+name "gemm_splitk", split-K aware op spec and score adjustment).  Split-K
+partials go to an fp32 workspace and are reduced deterministically instead of
+the reference's ``T.atomic_add`` into an uninitialised output (gemm.py:78).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, Dict, Optional
+
+import torch
+
+from ..autotuner.cost_model import make_matmul_spec
+from ..autotuner.gpu_spec import get_gpu_spec
+from ..autotuner.interface import select_best
+from .. import inputs as _inputs
+from .. import runtime
+from ._base import InstanceDescriptor
+
+
+class GemmDescriptor(InstanceDescriptor):
+    family = "gemm"
+    dtype = "f16"
+    split_k_values = (1, 2, 4)
+
+    @property
+    def name(self) -> str:
+        return "gemm_splitk"
+
+    def make_op_spec(self, raw_config=None, M=0, N=0, K=0, **kw):
+        sk = raw_config.get("split_k", 1) if raw_config else 1
+        return make_matmul_spec(M=M, N=N, K=K // sk, dtype=self.dtype)
+
+    def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
+        """Split-K pays an fp32 partial write + read per split and a reduction
+        launch: scale by t_mainloop / (t_mainloop + t_reduce) at roofline rates."""
+        sk = raw.get("split_k", 1)
+        if sk <= 1:
+            return base_score
+        hw = get_gpu_spec()
+        t_main = 2.0 * M * N * K / (hw.peak_tflops(self.dtype) * 1e12)
+        t_red = (2.0 * sk * M * N * 4 + M * N * 2) / (hw.mem_bandwidth_gbps * 1e9) + 4e-6
+        return base_score * t_main / (t_main + t_red)
+
+    # ---- tune() hooks ------------------------------------------------------
+    def make_inputs(self, M, N, K, **kw):
+        d = _inputs.config1(M, N, K, device="cuda")
+        d["C"] = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        return d
+
+    def make_runner(self, raw, inputs, M, N, K, **kw):
+        k = build_kernel(M, N, K, config=raw)
+        return lambda: k(inputs["A"], inputs["B"], out=inputs["C"])
+
+
+DESCRIPTOR = GemmDescriptor()
+
+
+def get_configs(M, K, split_k_values=(1, 2, 4), N: int = 0):
+    """Compiled candidates valid for this K (each K slice a multiple of block_K)."""
+    d = GemmDescriptor()
+    d.split_k_values = tuple(split_k_values)
+    return d.get_raw_configs(M=M, N=N, K=K)
+
+
+class CompiledGemm:
+    """A resolved instance bound to a shape: ``kernel(a, b) -> C`` (out_idx=[-1] convention)."""
+
+    def __init__(self, descriptor: InstanceDescriptor, M: int, N: int, K: int, config: Dict[str, Any],
+                 act: str = "none"):
+        self.descriptor, self.M, self.N, self.K, self.config, self.act = descriptor, M, N, K, config, act
+        self.inst = descriptor.instance_index(config)
+        self.split_k = config.get("split_k", 1)
+        self._ws: Optional[torch.Tensor] = None
+
+    def _workspace(self, device):
+        need = runtime.workspace_bytes(self.descriptor.family, self.inst, self.M, self.N, self.K, self.split_k)
+        if need and (self._ws is None or self._ws.device != device):
+            self._ws = runtime.alloc_workspace(need, device)
+        return self._ws
+
+    def __call__(self, a, b, bias=None, out=None, scale_a: float = 1.0, scale_b: float = 1.0):
+        return runtime.gemm(self.inst, self.descriptor.dtype, a, b, bias=bias, out=out, act=self.act,
+                            scale_a=scale_a, scale_b=scale_b, split_k=self.split_k,
+                            workspace=self._workspace(a.device))
+
+
+def build_kernel(M, N, K, config=None):
+    """Resolve a config (cost-model top-1 when None) to its compiled instance."""
+    if config is None:
+        config, _ = select_best(DESCRIPTOR, M=M, N=N, K=K)
+    return CompiledGemm(DESCRIPTOR, M, N, K, config)
+
+
+def flops(M, N, K) -> float:
+    return 2.0 * M * N * K
+
+
+__all__ = ["DESCRIPTOR", "CompiledGemm", "GemmDescriptor", "build_kernel", "flops", "get_configs"]

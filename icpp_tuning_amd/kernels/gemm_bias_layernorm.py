@@ -1,0 +1,129 @@
+"""Fused GEMM + bias + LayerNorm over N (fp16 in/out, fp32 statistics).
+
+Mirrors kernel/tilelang/gemm/gemm_bias_layernorm.py: ``get_gemm_configs``
+(:19-40), ``build_fused_kernel`` (:167-188, ``fused(A, B, bias, gamma, beta) ->
+Y``) and ``DESCRIPTOR`` (:196-208).  The reference launches a GEMM+bias kernel
+that writes X in fp32 and then a separate two-pass row LayerNorm kernel that
+reads X twice and computes var = E[x^2] - mean^2 (:143).  Two strategies here,
+chosen per shape by the tuner:
+
+  "row"       (gemm_ln_row)    one workgroup owns whole rows (N <= block_N):
+              mean and centred variance reduced in registers + LDS, no
+              intermediate in HBM, one launch.
+  "two_pass"  (gemm_ln_stats)  GEMM tiles write X (f16) into Y and a per-(row,
+              wave column block) (mean, M2) pair into the workspace; a finalize
+              pass merges the pairs (Chan et al.) and normalises Y in place.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Dict, List, Optional
+
+import torch
+
+from ..autotuner.cost_model import make_matmul_spec
+from ..autotuner.interface import select_best
+from .. import inputs as _inputs
+from .. import runtime
+from ._base import InstanceDescriptor, family_instances, raw_from_inst
+
+STRATEGY_FAMILY = {"row": "gemm_ln_row", "two_pass": "gemm_ln_stats"}
+
+
+class GemmBiasLayerNormDescriptor(InstanceDescriptor):
+    dtype = "f16"
+    family = "gemm_ln_stats"
+
+    @property
+    def name(self) -> str:
+        return "gemm_bias_layernorm"
+
+    def make_op_spec(self, raw_config=None, M=0, N=0, K=0, **kw):
+        return make_matmul_spec(M=M, N=N, K=K, primitives=["bias_add", "row_layernorm"], dtype=self.dtype)
+
+    def _family(self, raw) -> str:
+        return STRATEGY_FAMILY[raw.get("strategy", "two_pass")]
+
+    def instance_index(self, raw: Dict[str, Any]) -> int:
+        fam = self._family(raw)
+        mf = int(str(raw["mfma"]).split("x")[0])
+        for idx, inst in enumerate(family_instances(fam)):
+            if (inst.bm, inst.bn, inst.bk, inst.stages, inst.threads, inst.wm, inst.wn, inst.mf) == (
+                    raw["block_M"], raw["block_N"], raw["block_K"], raw["num_stages"], raw["thread_num"],
+                    raw["waves_m"], raw["waves_n"], mf):
+                return idx
+        raise KeyError(f"no compiled {fam} instance for {self.format_config(raw)}")
+
+    def instance_of(self, raw):
+        return family_instances(self._family(raw))[self.instance_index(raw)]
+
+    def get_raw_configs(self, **shape) -> List[Dict[str, Any]]:
+        K, N = shape["K"], shape.get("N", 0)
+        out = []
+        for strategy, fam in STRATEGY_FAMILY.items():
+            for inst in family_instances(fam):
+                if K % inst.bk:
+                    continue
+                if strategy == "row" and N and (N > inst.bn or inst.bn >= 2 * N):
+                    continue  # whole row must fit one tile without wasting half of it
+                raw = raw_from_inst(inst)
+                raw["strategy"] = strategy
+                out.append(raw)
+        return out
+
+    def format_config(self, raw):
+        return super().format_config(raw) + ("_ROW" if raw.get("strategy") == "row" else "_2P")
+
+    def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
+        """Two-pass pays one extra read + write of Y at HBM rate (roofline ratio)."""
+        if raw.get("strategy") == "row":
+            return base_score
+        from ..autotuner.gpu_spec import get_gpu_spec
+        hw = get_gpu_spec()
+        t_main = 2.0 * M * N * K / (hw.peak_tflops("f16") * 1e12)
+        t_fin = (2.0 * M * N * 2) / (hw.mem_bandwidth_gbps * 1e9) + 3e-6
+        return base_score * t_main / (t_main + t_fin)
+
+    def make_inputs(self, M, N, K, **kw):
+        d = _inputs.config3(M, N, K, device="cuda")
+        d["Y"] = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        return d
+
+    def make_runner(self, raw, inputs, M, N, K, **kw):
+        k = build_fused_kernel(M, N, K, gemm_config=raw)
+        return lambda: k(inputs["A"], inputs["B"], inputs["bias"], inputs["gamma"], inputs["beta"], out=inputs["Y"])
+
+
+DESCRIPTOR = GemmBiasLayerNormDescriptor()
+
+
+def get_gemm_configs(K, N: int = 0):
+    return DESCRIPTOR.get_raw_configs(K=K, N=N)
+
+
+class CompiledGemmLayerNorm:
+    def __init__(self, M, N, K, config, eps=1e-5):
+        self.M, self.N, self.K, self.config, self.eps = M, N, K, config, eps
+        self.family = STRATEGY_FAMILY[config.get("strategy", "two_pass")]
+        self.inst = DESCRIPTOR.instance_index(config)
+        self._ws: Optional[torch.Tensor] = None
+
+    def __call__(self, A, B, bias, gamma, beta, out=None):
+        need = runtime.workspace_bytes(self.family, self.inst, self.M, self.N, self.K)
+        if need and (self._ws is None or self._ws.device != A.device):
+            self._ws = runtime.alloc_workspace(need, A.device)
+        return runtime.gemm_bias_layernorm(self.family, self.inst, A, B, bias, gamma, beta, out=out,
+                                           eps=self.eps, workspace=self._ws)
+
+
+def build_fused_kernel(M, N, K, gemm_config=None, block_M_ln=16, block_N_ln=128, thread_num_ln=128, eps=1e-5):
+    """``fused(A, B, bias, gamma, beta) -> Y``.  The ``*_ln`` tile arguments of the
+    reference's standalone LN kernel are accepted for call compatibility; the
+    LayerNorm here is either fused into the GEMM epilogue or a fixed-geometry
+    finalize pass (one wave per row)."""
+    if gemm_config is None:
+        gemm_config, _ = select_best(DESCRIPTOR, M=M, N=N, K=K)
+    return CompiledGemmLayerNorm(M, N, K, gemm_config, eps=eps)
+
+
+__all__ = ["DESCRIPTOR", "GemmBiasLayerNormDescriptor", "STRATEGY_FAMILY", "build_fused_kernel", "get_gemm_configs"]

@@ -1,0 +1,122 @@
+"""Torch-facing launchers over the C ABI.
+
+PyTorch provides device memory and the stream; every launch goes through
+libicpp_hip.so.  Inputs are validated here (device, dtype, contiguity) so a
+mismatch is a Python exception rather than a fault; shape constraints are
+validated again by the library itself.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._lib import ACT, FAMILY, lib
+
+TORCH_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
+OUT_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.bfloat16}
+BIAS_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float32}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check(t: Optional[torch.Tensor], name: str, dtype: Optional[torch.dtype] = None, shape=None) -> int:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (got {t.device})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
+    return t.data_ptr()
+
+
+def workspace_bytes(family: str, inst: int, M: int, N: int, K: int, split_k: int = 1) -> int:
+    return lib().workspace_bytes(FAMILY[family], inst, M, N, K, split_k)
+
+
+def alloc_workspace(nbytes: int, device) -> Optional[torch.Tensor]:
+    if nbytes <= 0:
+        return None
+    return torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+
+
+def gemm(inst: int, dtype: str, a: torch.Tensor, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
+         out: Optional[torch.Tensor] = None, act: str = "none", scale_a: float = 1.0, scale_b: float = 1.0,
+         split_k: int = 1, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[M,N] = act(scale_a*scale_b * a[M,K] @ b[K,N] + bias[N]) through icpp_gemm."""
+    M, K = a.shape
+    K2, N = b.shape
+    if K2 != K:
+        raise ValueError(f"inner dimensions differ: a is {tuple(a.shape)}, b is {tuple(b.shape)}")
+    tdt = TORCH_DTYPE[dtype]
+    pa = _check(a, "a", tdt)
+    pb = _check(b, "b", tdt)
+    pbias = _check(bias, "bias", BIAS_DTYPE[dtype], (N,))
+    if out is None:
+        out = torch.empty((M, N), dtype=OUT_DTYPE[dtype], device=a.device)
+    pc = _check(out, "out", OUT_DTYPE[dtype], (M, N))
+    need = workspace_bytes("gemm", inst, M, N, K, split_k)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = alloc_workspace(need, a.device)
+    pws = workspace.data_ptr() if (need and workspace is not None) else None
+    wsb = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
+    lib().call("icpp_gemm", inst, pa, pb, pbias, pc, M, N, K, K, N, N, ACT[act],
+               float(scale_a), float(scale_b), split_k, pws, wsb, _stream())
+    return out
+
+
+def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor, bias: Optional[torch.Tensor],
+                        gamma: torch.Tensor, beta: torch.Tensor, out: Optional[torch.Tensor] = None,
+                        eps: float = 1e-5, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = LayerNorm_N(a @ b + bias) * gamma + beta through icpp_gemm_bias_layernorm (f16)."""
+    M, K = a.shape
+    _, N = b.shape
+    h = torch.float16
+    pa, pb = _check(a, "a", h), _check(b, "b", h, (K, N))
+    pbias = _check(bias, "bias", h, (N,))
+    pg, pbe = _check(gamma, "gamma", h, (N,)), _check(beta, "beta", h, (N,))
+    if out is None:
+        out = torch.empty((M, N), dtype=h, device=a.device)
+    py = _check(out, "out", h, (M, N))
+    need = workspace_bytes(family, inst, M, N, K, 1)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = alloc_workspace(need, a.device)
+    pws = workspace.data_ptr() if (need and workspace is not None) else None
+    wsb = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
+    lib().call("icpp_gemm_bias_layernorm", FAMILY[family], inst, pa, pb, pbias, pg, pbe, py,
+               M, N, K, float(eps), pws, wsb, _stream())
+    return out
+
+
+def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, stride: int = 1, pad: int = 1,
+                dilation: int = 1, split_k: int = 1, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y[N,OH,OW,F] = conv2d(x[N,H,W,C], w[KH,KW,C,F]) through icpp_conv2d_nhwc (f16)."""
+    N, H, W, C = x.shape
+    KH, KW, C2, F = w.shape
+    if C2 != C:
+        raise ValueError(f"channel mismatch: x has C={C}, w has C={C2}")
+    OH = (H + 2 * pad - dilation * (KH - 1) - 1) // stride + 1
+    OW = (W + 2 * pad - dilation * (KW - 1) - 1) // stride + 1
+    h = torch.float16
+    px, pw = _check(x, "x", h), _check(w, "w", h)
+    py = _check(y, "y", h, (N, OH, OW, F))
+    Mg, Kg = N * OH * OW, KH * KW * C
+    need = workspace_bytes("conv2d", inst, Mg, F, Kg, split_k)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = alloc_workspace(need, x.device)
+    pws = workspace.data_ptr() if (need and workspace is not None) else None
+    wsb = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
+    lib().call("icpp_conv2d_nhwc", inst, px, pw, py, N, H, W, C, F, KH, KW, stride, pad, dilation,
+               split_k, pws, wsb, _stream())
+    return y
+
+
+__all__ = ["BIAS_DTYPE", "OUT_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
+           "gemm_bias_layernorm", "workspace_bytes"]

@@ -1,0 +1,117 @@
+/*
+ * icpp_hip.h -- C ABI of libicpp_hip.so, the gfx950 (MI355X) kernel library
+ * behind the tuner's "compile / run / benchmark" steps.
+ *
+ * The reference binds its device code in-process through TileLang: each kernel
+ * module compiles a shape-specialised prim_func and calls it on torch tensors
+ * (kernel/tilelang/gemm/gemm.py:84-89, gemm_bias_act.py:91-96,
+ * gemm_bias_layernorm.py:167-188, conv/conv2d.py:282-290).  Here the kernels are
+ * compiled ahead of time as a fixed set of tile instances; "compile" resolves a
+ * config to an instance index and "run" is one of the launchers below.
+ *
+ * Conventions
+ *  - Plain C types only; tensors are device pointers, row-major, contiguous.
+ *  - Return 0 on success, a negative ICPP_E_* code on a rejected call, or a
+ *    positive hipError_t from the launch.  icpp_last_error() describes the last
+ *    failure of the calling thread.
+ *  - Launchers never allocate device memory: split-K partials and LayerNorm
+ *    statistics live in a caller-owned workspace of icpp_workspace_bytes().
+ *  - Launches are asynchronous on `stream` (a hipStream_t; NULL = default).
+ *  - Stateless and reentrant; concurrent calls may share instances.
+ */
+#ifndef ICPP_HIP_H
+#define ICPP_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ICPP_ABI_VERSION 1
+
+/* instance families */
+enum icpp_family {
+  ICPP_FAMILY_GEMM = 0,        /* dense GEMM, epilogue bias/act or split-K partials */
+  ICPP_FAMILY_GEMM_LN_STATS = 1,/* GEMM+bias writing X and per-(row, column block) LN statistics */
+  ICPP_FAMILY_GEMM_LN_ROW = 2, /* GEMM+bias+LayerNorm with whole rows per workgroup */
+  ICPP_FAMILY_CONV2D = 3,      /* NHWC x HWIO implicit-GEMM conv2d */
+  ICPP_NUM_FAMILIES = 4
+};
+
+enum icpp_dtype { ICPP_F16 = 0, ICPP_BF16 = 1, ICPP_FP8_E4M3 = 2 };
+enum icpp_act { ICPP_ACT_NONE = 0, ICPP_ACT_RELU = 1, ICPP_ACT_GELU_TANH = 2, ICPP_ACT_SILU = 3 };
+
+enum icpp_status {
+  ICPP_OK = 0,
+  ICPP_E_INSTANCE = -1,  /* bad family / instance index */
+  ICPP_E_SHAPE = -2,     /* shape not supported by the instance (divisibility, alignment) */
+  ICPP_E_WORKSPACE = -3, /* workspace missing or too small */
+  ICPP_E_ARG = -4        /* other invalid argument */
+};
+
+typedef struct icpp_tile {
+  int family;      /* enum icpp_family */
+  int dtype;       /* enum icpp_dtype of A and B */
+  int block_m, block_n, block_k;
+  int waves_m, waves_n;
+  int stages;      /* LDS buffers */
+  int mfma_m, mfma_n, mfma_k;
+  int lds_bytes;   /* static LDS of the mainloop kernel */
+  int threads;
+  char name[96];
+} icpp_tile_t;
+
+int icpp_abi_version(void);
+const char* icpp_last_error(void);
+
+/* Instance table: the tuner's candidate space (replaces get_configs(), gemm.py:24-48). */
+int icpp_num_instances(int family);
+int icpp_instance_info(int family, int idx, icpp_tile_t* out);
+
+/* Bytes of workspace a call needs (0 when none). */
+size_t icpp_workspace_bytes(int family, int inst, int M, int N, int K, int split_k);
+
+/*
+ * C[M,N] = act(scale_a*scale_b * A[M,K].B[K,N] + bias[N]).
+ * Replaces the TileLang kernels of gemm.py:61-79 (bias = NULL, act = NONE) and
+ * gemm_bias_act.py:59-86 (bias + ReLU), and adds GELU-tanh / SiLU and the fp8
+ * e4m3 per-tensor-scaled variant.  Output and bias dtypes follow the instance
+ * dtype: f16 -> f16 out/bias, bf16 -> bf16 out/bias, fp8 -> bf16 out, f32 bias.
+ * split_k > 1 accumulates K slices in the fp32 workspace and reduces them.
+ * Requires K % (block_k * split_k) == 0, N % 8 == 0, ld* % 8 == 0.
+ */
+int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
+              int M, int N, int K, int lda, int ldb, int ldc, int act,
+              float scale_a, float scale_b, int split_k,
+              void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Y[M,N] = LayerNorm_N(A.B + bias) * gamma + beta, f16 in / f16 out, fp32 statistics.
+ * Replaces build_fused_kernel (gemm_bias_layernorm.py:167-188: GEMM+bias kernel
+ * :61-88 followed by the row LayerNorm kernel :101-162).  `family` selects the
+ * strategy: ICPP_FAMILY_GEMM_LN_ROW (whole row per workgroup, N <= block_n,
+ * no workspace) or ICPP_FAMILY_GEMM_LN_STATS (GEMM writes X into Y plus
+ * per-block (mean, M2) into the workspace, then a finalize pass normalises Y).
+ */
+int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
+                             const void* gamma, const void* beta, void* Y,
+                             int M, int N, int K, float eps,
+                             void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Y[N,OH,OW,F] = conv2d(X[N,H,W,C], W[KH,KW,C,F]), f16, fp32 accumulate.
+ * Replaces make_conv2d_kernel / build_conv2d_kernel (conv2d.py:208-290):
+ * destination-passing like the reference's kernel(X, W, Y).
+ * Requires C % 8 == 0, F % 8 == 0, (KH*KW*C) % (block_k * split_k) == 0.
+ */
+int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
+                     int N, int H, int W, int C, int F, int KH, int KW,
+                     int stride, int pad, int dilation, int split_k,
+                     void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ICPP_HIP_H */

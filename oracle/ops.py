@@ -1,0 +1,98 @@
+"""fp32 CPU restatement of the reference's torch programs for each fused op.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+FP8_MAX = 448.0  # OCP e4m3fn largest finite value
+
+
+def gemm_ref(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """C = A @ B with fp32 accumulation (reference gemm.py:19-21 computes
+    ``(A @ B).to(float32)``; restated in fp32 on CPU)."""
+    return A.float().cpu() @ B.float().cpu()
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) -- reference evaluation/end2end.py:37-38."""
+    return 0.5 * x * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * torch.pow(x, 3.0))))
+
+
+def apply_act(x: torch.Tensor, act: str) -> torch.Tensor:
+    if act == "none":
+        return x
+    if act == "relu":
+        return torch.clamp_min(x, 0.0)                 # gemm_bias_act.py:47 torch.relu
+    if act in ("gelu_tanh", "gelu"):
+        return gelu_tanh(x)
+    if act == "silu":
+        return x * torch.sigmoid(x)                    # SiLU = x * sigmoid(x)
+    raise ValueError(act)
+
+
+def gemm_bias_act_ref(A, B, bias, act: str = "relu") -> torch.Tensor:
+    """act(A @ B + bias) in fp32 -- reference gemm_bias_act.py:43-47 (ReLU), with the
+    GELU-tanh / SiLU epilogues the build adds."""
+    x = gemm_ref(A, B)
+    if bias is not None:
+        x = x + bias.float().cpu().unsqueeze(0)
+    return apply_act(x, act)
+
+
+def gemm_bias_layernorm_ref(A, B, bias, gamma, beta, eps: float = 1e-5) -> torch.Tensor:
+    """layer_norm(A @ B + bias, (N,), gamma, beta, eps) in fp32 -- reference
+    gemm_bias_layernorm.py:43-49 (torch_baseline)."""
+    x = gemm_ref(A, B)
+    if bias is not None:
+        x = x + bias.float().cpu().unsqueeze(0)
+    mean = x.mean(dim=1, keepdim=True)
+    var = ((x - mean) ** 2).mean(dim=1, keepdim=True)  # biased variance, two-pass
+    return (x - mean) * torch.rsqrt(var + eps) * gamma.float().cpu() + beta.float().cpu()
+
+
+def conv2d_nhwc_ref(X, Wt, stride: int = 1, padding: int = 1, dilation: int = 1) -> torch.Tensor:
+    """NHWC x HWIO conv2d in fp32 -- reference conv2d.py:35-62 (permute to NCHW/OIHW,
+    F.conv2d, permute back)."""
+    x = X.float().cpu().permute(0, 3, 1, 2)
+    w = Wt.float().cpu().permute(3, 2, 0, 1)
+    y = F.conv2d(x, w, stride=stride, padding=padding, dilation=dilation)
+    return y.permute(0, 2, 3, 1).contiguous()
+
+
+def conv_out_hw(H, W, KH, KW, S, P, D=1):
+    """reference conv2d.py:65-68"""
+    return (H + 2 * P - D * (KH - 1) - 1) // S + 1, (W + 2 * P - D * (KW - 1) - 1) // S + 1
+
+
+def quantize_fp8(x: torch.Tensor):
+    """Per-tensor e4m3fn quantisation with scale = amax / 448."""
+    x = x.float()
+    amax = x.abs().max().clamp_min(1e-12)
+    scale = (amax / FP8_MAX).item()
+    q = (x / scale).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q, scale
+
+
+def fp8_gemm_bias_act_ref(Aq, Bq, scale_a: float, scale_b: float, bias, act: str = "silu") -> torch.Tensor:
+    """act(scale_a*scale_b * deq(Aq) @ deq(Bq) + bias) in fp32 (no reference kernel exists;
+    this is the dequantised-fp32 oracle BASELINE.json names for config 5)."""
+    a = Aq.cpu().float()
+    b = Bq.cpu().float()
+    x = (a @ b) * (scale_a * scale_b)
+    if bias is not None:
+        x = x + bias.float().cpu().unsqueeze(0)
+    return apply_act(x, act)
+
+
+def op_flops(op: str, **s) -> float:
+    """Algorithmic mainloop FLOPs (reference gemm_bias_act.py:139, conv2d.py:71-72)."""
+    if op == "conv2d":
+        OH, OW = conv_out_hw(s["H"], s["W"], s["KH"], s["KW"], s.get("S", 1), s.get("P", 1))
+        return 2.0 * s["N"] * OH * OW * s["F"] * s["C"] * s["KH"] * s["KW"]
+    return 2.0 * s["M"] * s["N"] * s["K"]

@@ -1,0 +1,83 @@
+"""The C ABI library: loads without a GPU, exports every declared symbol, its
+instance table matches instances.py, and argument validation rejects bad
+calls before anything is launched (no device work happens in these tests)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from icpp_tuning_amd import _lib
+from icpp_tuning_amd.instances import INSTANCES
+from icpp_tuning_amd.kernels._base import family_instances
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "icpp_hip.h"
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def test_header_symbols_are_exported(L):
+    declared = set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(icpp_\w+)\s*\(", HEADER.read_text(), re.M))
+    assert declared == set(_lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert L.has_symbol(name), name
+
+
+def test_abi_version(L):
+    assert L._dll.icpp_abi_version() == _lib.ABI_VERSION
+
+
+def test_instance_table_matches_python_list(L):
+    for fam, fid in _lib.FAMILY.items():
+        rows = L.instances(fid)
+        expect = family_instances(fam)
+        assert [r["name"] for r in rows] == [i.name for i in expect]
+        for r, i in zip(rows, expect):
+            assert (r["block_m"], r["block_n"], r["block_k"], r["waves_m"], r["waves_n"], r["stages"], r["mfma_m"]) == (
+                i.bm, i.bn, i.bk, i.wm, i.wn, i.stages, i.mf)
+            assert r["lds_bytes"] == i.lds_bytes and r["threads"] == i.threads
+    assert sum(len(L.instances(f)) for f in _lib.FAMILY.values()) == len(INSTANCES)
+
+
+def test_resources_recorded_for_every_instance():
+    res = _lib.resources()
+    for i in INSTANCES:
+        r = res[i.name]
+        assert r["lds"] == i.lds_bytes
+        assert r["vgprs"] + r["agprs"] <= 512
+
+
+def test_workspace_bytes(L):
+    gemm0 = 0
+    assert L.workspace_bytes(_lib.FAMILY["gemm"], gemm0, 128, 256, 512, 1) == 0
+    assert L.workspace_bytes(_lib.FAMILY["gemm"], gemm0, 128, 256, 512, 4) == 4 * 128 * 256 * 4
+    st = family_instances("gemm_ln_stats")[0]
+    cols = -(-1000 // (st.bn // st.wn))
+    assert L.workspace_bytes(_lib.FAMILY["gemm_ln_stats"], 0, 64, 1000, 512, 1) == 64 * cols * 2 * 4
+
+
+def _gemm_call(L, inst=0, A=16, B=16, C=16, M=64, N=64, K=64, ldc=None, split=1, ws=None, wsb=0, act=0):
+    f = L._dll.icpp_gemm
+    return f(inst, A, B, None, C, M, N, K, K, N, N if ldc is None else ldc, act, 1.0, 1.0, split, ws, wsb, None)
+
+
+def test_validation_errors_before_launch(L):
+    # null tensors, bad instance, bad shapes, missing workspace: all rejected on the host
+    assert _gemm_call(L, A=None) == -4
+    assert _gemm_call(L, inst=10 ** 6) == -1
+    assert _gemm_call(L, N=60) == -2           # N % 8
+    assert _gemm_call(L, K=40) == -2           # K not a multiple of block_k
+    assert _gemm_call(L, act=9) == -4
+    assert _gemm_call(L, split=2, K=256) == -3  # split-K without workspace
+    assert _gemm_call(L, A=17) == -4           # misaligned pointer
+    assert "aligned" in L.last_error()
+    f = L._dll.icpp_gemm_bias_layernorm
+    assert f(7, 0, 16, 16, None, 16, 16, 16, 64, 64, 64, 1e-5, None, 0, None) == -1
+    row = _lib.FAMILY["gemm_ln_row"]
+    assert f(row, 0, 16, 16, None, 16, 16, 16, 64, 2048, 64, 1e-5, None, 0, None) == -2  # N > block_n
+    c = L._dll.icpp_conv2d_nhwc
+    assert c(0, 16, 16, 16, 1, 8, 8, 3, 64, 3, 3, 1, 1, 1, 1, None, 0, None) == -2  # C % 8

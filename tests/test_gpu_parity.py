@@ -1,0 +1,192 @@
+"""GPU parity: every compiled instance against the CPU oracle on seeded inputs.
+
+Tolerances (stated per op, checked elementwise as |y - y_ref| <= atol + rtol*|y_ref|):
+  GEMM / GEMM+bias+act (fp16, bf16)     rtol 1e-2, atol 1e-2  (reference gemm_bias_act.py:160)
+  conv2d (fp16)                          rtol 1e-2, atol 1e-2  (reference conv2d.py:310)
+  GEMM+bias+LayerNorm (fp16 out)         atol 2e-2, rtol 2e-2
+  fp8 e4m3 GEMM+bias+SiLU (bf16 out)     rtol 1e-2, atol 1e-2 against the oracle run on
+                                         the same dequantised fp8 values (scale = amax/448)
+"""
+
+import math
+
+import pytest
+import torch
+
+from icpp_tuning_amd import inputs as I
+from icpp_tuning_amd import runtime
+from icpp_tuning_amd.kernels import conv2d as conv_mod
+from icpp_tuning_amd.kernels import fp8_gemm_bias_act as fp8_mod
+from icpp_tuning_amd.kernels import gemm as gemm_mod
+from icpp_tuning_amd.kernels import gemm_bias_act as gba_mod
+from icpp_tuning_amd.kernels import gemm_bias_layernorm as ln_mod
+from icpp_tuning_amd.kernels._base import family_instances, raw_from_inst
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(y, ref, rtol, atol, what):
+    y = y.float().cpu()
+    ref = ref.float().cpu()
+    assert y.shape == ref.shape, what
+    assert torch.isfinite(y).all(), f"{what}: non-finite output"
+    err = (y - ref).abs()
+    bound = atol + rtol * ref.abs()
+    bad = (err > bound)
+    if bad.any():
+        idx = bad.nonzero()[0].tolist()
+        raise AssertionError(f"{what}: {int(bad.sum())} / {y.numel()} outside tol; max err {err.max().item():.4g}; "
+                             f"first at {idx}: got {y[tuple(idx)].item():.5g} want {ref[tuple(idx)].item():.5g}")
+
+
+def _gemm_inst_ids(dtype):
+    return [(i, inst.name) for i, inst in enumerate(family_instances("gemm")) if inst.dtype == dtype]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_every_gemm_instance(gpu, dtype):
+    """All compiled GEMM tiles at a ragged shape: M not a tile multiple, bias + act."""
+    M, N, K = 200, 328, 512
+    tdt = runtime.TORCH_DTYPE[dtype]
+    d = I.gemm_inputs(M, N, K, tdt, 90, b_std=1 / math.sqrt(K), bias=True)
+    for act in ("none", "relu", "gelu_tanh", "silu"):
+        ref = O.gemm_bias_act_ref(d["A"], d["B"], d["bias"], act)
+        A, B, bias = d["A"].cuda(), d["B"].cuda(), d["bias"].cuda()
+        for idx, name in _gemm_inst_ids(dtype):
+            inst = family_instances("gemm")[idx]
+            if K % inst.bk:
+                continue
+            print(f"[parity] {name} act={act} M={M} N={N} K={K}", flush=True)
+            y = runtime.gemm(idx, dtype, A, B, bias=bias, act=act)
+            torch.cuda.synchronize()
+            _close(y, ref, 1e-2, 1e-2, f"{name} act={act}")
+
+
+@pytest.mark.parametrize("M", [1, 6, 61, 126])
+def test_reference_eval_shapes_splitk(gpu, M):
+    """The reference's evaluation shapes (M=1..126, N=2304, K=768), fp16, split-K 1/2/4."""
+    N, K = 2304, 768
+    d = I.gemm_inputs(M, N, K, torch.float16, 91)
+    ref = O.gemm_ref(d["A"], d["B"])
+    A, B = d["A"].cuda(), d["B"].cuda()
+    for raw in gemm_mod.get_configs(M, K, split_k_values=(1, 2, 4), N=N):
+        k = gemm_mod.build_kernel(M, N, K, config=raw)
+        print(f"[parity] gemm {gemm_mod.DESCRIPTOR.format_config(raw)} M={M}", flush=True)
+        y = k(A, B)
+        torch.cuda.synchronize()
+        _close(y, ref, 1e-2, 1e-2, f"gemm {raw} M={M}")
+
+
+def test_config1_gemm_1024(gpu):
+    M = N = K = 1024
+    d = I.config1()
+    ref = O.gemm_ref(d["A"], d["B"])
+    k = gemm_mod.build_kernel(M, N, K)
+    y = k(d["A"].cuda(), d["B"].cuda())
+    torch.cuda.synchronize()
+    _close(y, ref, 1e-2, 1e-2, f"config1 {k.config}")
+
+
+@pytest.mark.parametrize("act", ["gelu_tanh", "relu", "silu"])
+def test_config2_gemm_bias_act_4096(gpu, act):
+    M = N = K = 4096
+    d = I.config2()
+    ref = O.gemm_bias_act_ref(d["A"], d["B"], d["bias"], act)
+    k = gba_mod.build_kernel(M, N, K, act=act, dtype="bf16")
+    print(f"[parity] config2 {act} {k.config}", flush=True)
+    y = k(d["A"].cuda(), d["B"].cuda(), d["bias"].cuda())
+    torch.cuda.synchronize()
+    _close(y, ref, 1e-2, 1e-2, f"config2 {act} {k.config}")
+
+
+@pytest.mark.parametrize("strategy", ["row", "two_pass"])
+def test_every_ln_instance(gpu, strategy):
+    M, K = 333, 512
+    fam = ln_mod.STRATEGY_FAMILY[strategy]
+    for idx, inst in enumerate(family_instances(fam)):
+        N = 768 if (strategy == "row" and inst.bn == 768) else (1024 if strategy == "row" else 776)
+        d = I.config3(M, N, K)
+        ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+        raw = raw_from_inst(inst)
+        raw["strategy"] = strategy
+        print(f"[parity] {inst.name} M={M} N={N} K={K}", flush=True)
+        k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+        y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
+        torch.cuda.synchronize()
+        _close(y, ref, 2e-2, 2e-2, inst.name)
+
+
+@pytest.mark.parametrize("N", [768, 1024, 4096])
+def test_config3_gemm_bias_layernorm(gpu, N):
+    M, K = 8192, 4096
+    d = I.config3(M, N, K)
+    ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+    k = ln_mod.build_fused_kernel(M, N, K)
+    print(f"[parity] config3 N={N} {k.config}", flush=True)
+    y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
+    torch.cuda.synchronize()
+    _close(y, ref, 2e-2, 2e-2, f"config3 N={N} {k.config}")
+
+
+def test_every_conv_instance(gpu):
+    Nb, H, W, C, F = 2, 9, 7, 64, 64
+    d = I.config4(Nb, H, W, C, F)
+    ref = O.conv2d_nhwc_ref(d["X"], d["W"], 1, 1)
+    X, Wt = d["X"].cuda(), d["W"].cuda()
+    for idx, inst in enumerate(family_instances("conv2d")):
+        for sk in (1, 3):
+            if (9 * C) % (inst.bk * sk):
+                continue
+            raw = raw_from_inst(inst, sk)
+            print(f"[parity] {inst.name} sk={sk}", flush=True)
+            k = conv_mod.build_conv2d_kernel(Nb, C, H, W, F, 3, 3, 1, 1, 1, config=raw)
+            Y = torch.full((Nb, H, W, F), float("nan"), dtype=torch.float16, device="cuda")
+            k(X, Wt, Y)
+            torch.cuda.synchronize()
+            _close(Y, ref, 1e-2, 1e-2, f"{inst.name} sk={sk}")
+
+
+@pytest.mark.parametrize("shape", [(32, 56, 56, 64, 64), (32, 14, 14, 256, 256), (32, 7, 7, 512, 512),
+                                   (3, 5, 5, 64, 24)])
+def test_config4_conv(gpu, shape):
+    Nb, H, W, C, F = shape
+    d = I.config4(Nb, H, W, C, F)
+    ref = O.conv2d_nhwc_ref(d["X"], d["W"], 1, 1)
+    k = conv_mod.build_conv2d_kernel(Nb, C, H, W, F, 3, 3, 1, 1, 1)
+    print(f"[parity] config4 {shape} {k.config}", flush=True)
+    Y = torch.empty((Nb, H, W, F), dtype=torch.float16, device="cuda")
+    k(d["X"].cuda(), d["W"].cuda(), Y)
+    torch.cuda.synchronize()
+    _close(Y, ref, 1e-2, 1e-2, f"config4 {shape} {k.config}")
+
+
+def test_every_fp8_instance(gpu):
+    M, N, K = 40, 512, 1024
+    d = I.config5(M, N, K)
+    ref = O.fp8_gemm_bias_act_ref(d["A"], d["B"], d["scale_a"], d["scale_b"], d["bias"], "silu")
+    A, B, bias = d["A"].cuda(), d["B"].cuda(), d["bias"].cuda()
+    for idx, inst in enumerate(family_instances("gemm")):
+        if inst.dtype != "fp8":
+            continue
+        for sk in (1, 2):
+            if K % (inst.bk * sk):
+                continue
+            print(f"[parity] {inst.name} sk={sk}", flush=True)
+            y = runtime.gemm(idx, "fp8", A, B, bias=bias, act="silu", scale_a=d["scale_a"], scale_b=d["scale_b"],
+                             split_k=sk)
+            torch.cuda.synchronize()
+            _close(y, ref, 1e-2, 1e-2, f"{inst.name} sk={sk}")
+
+
+@pytest.mark.parametrize("M", [16, 256, 4096])
+@pytest.mark.parametrize("NK", [(4096, 4096), (11008, 4096), (4096, 11008)])
+def test_config5_fp8(gpu, M, NK):
+    N, K = NK
+    d = I.config5(M, N, K)
+    ref = O.fp8_gemm_bias_act_ref(d["A"], d["B"], d["scale_a"], d["scale_b"], d["bias"], "silu")
+    k = fp8_mod.build_kernel(M, N, K)
+    print(f"[parity] config5 M={M} N={N} K={K} {k.config}", flush=True)
+    y = k(d["A"].cuda(), d["B"].cuda(), d["scale_a"], d["scale_b"], d["bias"].cuda())
+    torch.cuda.synchronize()
+    _close(y, ref, 1e-2, 1e-2, f"config5 M={M} N={N} K={K}")
