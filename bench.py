@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 fused-kernel hot path on one MI355X.
+
+Headline (BASELINE.json metric, config 2): fused GEMM + bias + GELU(tanh),
+M = N = K = 4096, bf16 in / bf16 out, fp32 accumulate, seeded synthetic
+inputs resident in HBM.  A "step" is one launch of the fused op; ``value`` is
+2*M*N*K*steps / (timed wall time) in TFLOP/s.
+
+The same JSON line also carries
+  roofline      the kernel's average duration from HIP events on its stream,
+                against the dense bf16 MFMA peak (2516.6 TFLOP/s)
+  cpu_baseline  the CPU oracle (fp32 eager torch, oracle/ops.py) on a bounded
+                row-slice of the same problem, on this host's cores
+  ops           TFLOP/s and % of peak (or GB/s and % of 8 TB/s for HBM-bound
+                shapes) for every benchmark configuration, with the tuner's
+                time-to-best (prune + rank, compile = 0 for AOT instances,
+                top-k device benchmark)
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--quick] [--no-ops]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "TFLOP/s and % MFMA peak per fused op on 1 MI355X; tuner time-to-best"
+PEAK_BF16 = 2516.6
+PEAK_FP8 = 5033.2
+HBM_GBPS = 8000.0
+
+
+def _events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Warm up, then time exactly `steps` calls bracketed by synchronize."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = _events()
+    t0 = time.perf_counter()
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, s.elapsed_time(e) / 1e3
+
+
+def cpu_baseline(target_seconds: float = 12.0):
+    """Oracle GEMM+bias+GELU on CPU over a row slice of config 2, median of 3."""
+    import torch
+
+    from icpp_tuning_amd import inputs as I
+    from oracle import ops as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    K = N = 4096
+    probe_rows = 256
+    d = I.config2(4096, N, K)
+    A, B, bias = d["A"], d["B"], d["bias"]
+    t0 = time.perf_counter()
+    O.gemm_bias_act_ref(A[:probe_rows], B, bias, "gelu_tanh")
+    per_row = (time.perf_counter() - t0) / probe_rows
+    rows = int(max(probe_rows, min(4096, target_seconds / 3.0 / max(per_row, 1e-9))))
+    rows = max(probe_rows, rows // 64 * 64)
+    O.gemm_bias_act_ref(A[:rows], B, bias, "gelu_tanh")  # warmup
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.gemm_bias_act_ref(A[:rows], B, bias, "gelu_tanh")
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    tflops = 2.0 * rows * N * K / ts[1] / 1e12
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle gemm_bias_act_ref(gelu_tanh) fp32 eager on CPU, rows 0..{rows} of the 4096^3 "
+                      f"bf16 config-2 inputs (M={rows}, N=K=4096), median of 3 after 1 warmup"}
+
+
+def _load_traffic(workload: str):
+    p = ROOT / "profiles" / f"traffic_{workload}.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+def bench_ops(quick: bool):
+    """Every benchmark configuration: tuned config, TFLOP/s, fraction of its roofline."""
+    import torch
+
+    from icpp_tuning_amd.autotuner.interface import benchmark_ms, tune
+    from icpp_tuning_amd.kernels import conv2d as CV
+    from icpp_tuning_amd.kernels import fp8_gemm_bias_act as F8
+    from icpp_tuning_amd.kernels import gemm as G
+    from icpp_tuning_amd.kernels import gemm_bias_act as GBA
+    from icpp_tuning_amd.kernels import gemm_bias_layernorm as LN
+
+    rows = []
+    top_k = 2 if quick else 4
+
+    def record(op, desc, shape, flops, min_bytes, dtype, **extra):
+        t0 = time.perf_counter()
+        res = tune(desc, top_k=top_k, warmup=2, reps=5, **shape)
+        inputs = desc.make_inputs(**shape)
+        run = desc.make_runner(res.best_config, inputs, **shape)
+        ms = benchmark_ms(run, warmup=3, reps=20)
+        del inputs
+        tflops = flops / ms / 1e9
+        gbps = min_bytes / ms / 1e6
+        peak = PEAK_FP8 if dtype == "fp8" else PEAK_BF16
+        ridge = peak * 1e3 / HBM_GBPS
+        bound = "mfma" if flops / min_bytes >= ridge else "hbm"
+        row = {"op": op, "shape": shape, "dtype": dtype, "config": desc.format_config(res.best_config),
+               "ms": round(ms, 5), "tflops": round(tflops, 2), "pct_mfma_peak": round(100 * tflops / peak, 2),
+               "gbps": round(gbps, 1), "pct_hbm": round(100 * gbps / HBM_GBPS, 2), "bound": bound,
+               "formula_top1": desc.format_config(res.formula_top1),
+               "formula_top1_ms": round(res.formula_top1_ms, 5),
+               "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),
+                         "compile_s": round(res.compile_s, 4), "bench_s": round(res.bench_s, 3),
+                         "candidates": len(res.candidates), "n_configs": res.n_configs, "n_pruned": res.n_pruned}}
+        row.update(extra)
+        rows.append(row)
+        print(f"[bench] {op} {shape} {row['config']}: {ms*1e3:.1f} us, {tflops:.1f} TFLOP/s "
+              f"({row['pct_mfma_peak']}% peak), {gbps:.0f} GB/s, tuned in {res.time_to_best_s:.2f}s",
+              file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+
+    M = N = K = 1024
+    record("gemm", G.DESCRIPTOR, dict(M=M, N=N, K=K), 2.0 * M * N * K, 2 * (M * K + K * N + M * N), "f16")
+    acts = ["gelu_tanh"] if quick else ["gelu_tanh", "relu", "silu"]
+    for act in acts:
+        M = N = K = 4096
+        record(f"gemm_bias_{act}", GBA.descriptor(act, "bf16"), dict(M=M, N=N, K=K), 2.0 * M * N * K,
+               2 * (M * K + K * N + M * N) + 2 * N, "bf16")
+    for Nn in ([4096] if quick else [768, 1024, 4096]):
+        M, K = 8192, 4096
+        record("gemm_bias_layernorm", LN.DESCRIPTOR, dict(M=M, N=Nn, K=K), 2.0 * M * Nn * K,
+               2 * (M * K + K * Nn + M * Nn) + 6 * Nn, "f16")
+    convs = [(32, 56, 56, 64, 64)] if quick else [(32, 56, 56, 64, 64), (32, 14, 14, 256, 256), (32, 7, 7, 512, 512)]
+    for (Nb, H, W, C, F) in convs:
+        shape = dict(N=Nb, C=C, H=H, W=W, OC=F, KH=3, KW=3, stride=1, padding=1)
+        record("conv2d", CV.DESCRIPTOR, shape, float(CV.calc_conv_flops(Nb, C, H, W, F, 3, 3)),
+               2 * (Nb * H * W * C + 9 * C * F + Nb * H * W * F), "f16")
+    f8_shapes = [(16, 4096, 4096), (4096, 4096, 4096)] if quick else [
+        (m, n, k) for m in (16, 256, 4096) for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008))]
+    for (M, N, K) in f8_shapes:
+        record("fp8_gemm_bias_silu", F8.DESCRIPTOR, dict(M=M, N=N, K=K), 2.0 * M * N * K,
+               M * K + K * N + 2 * M * N + 4 * N, "fp8")
+    return rows
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="fewer per-op rows")
+    ap.add_argument("--no-ops", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--headline-only-kernel", action="store_true",
+                    help="tune + time the headline kernel only (for profiler runs)")
+    ap.add_argument("--instance", default=None,
+                    help="time this compiled GEMM instance (by name) instead of the tuned one")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": src.numel() * 4, "calibrate_copy_bytes_written": dst.numel() * 4}))
+        return 0
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
+              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from icpp_tuning_amd import inputs as I
+    from icpp_tuning_amd.autotuner.interface import select_best
+    from icpp_tuning_amd.kernels import gemm_bias_act as GBA
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    M = N = K = 4096
+    desc = GBA.descriptor("gelu_tanh", "bf16")
+    t_sel = time.perf_counter()
+    cfg, score = select_best(desc, M=M, N=N, K=K)
+    select_s = time.perf_counter() - t_sel
+    # the tuned choice for this shape (measured top-k); fall back to the formula top-1
+    from icpp_tuning_amd.autotuner.interface import tune
+
+    if args.instance:
+        from icpp_tuning_amd.kernels._base import family_instances, raw_from_inst
+
+        match = [i for i in family_instances("gemm") if i.name == args.instance]
+        if not match:
+            print(f"bench.py: unknown instance {args.instance}", file=sys.stderr)
+            return 2
+        cfg, tuned = raw_from_inst(match[0]), None
+    else:
+        res = tune(desc, top_k=4, warmup=2, reps=5, M=M, N=N, K=K)
+        cfg, tuned = res.best_config, res
+    kern = GBA.build_kernel(M, N, K, config=cfg, act="gelu_tanh", dtype="bf16")
+    d = I.config2(M, N, K, device="cuda")
+    A, B, bias = d["A"], d["B"], d["bias"]
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    step = lambda: kern(A, B, bias, out=C)  # noqa: E731
+    wall, ev = time_steps(step, args.steps, args.warmup)
+    flops = 2.0 * M * N * K
+    value = flops * args.steps / wall / 1e12
+    achieved = flops / (ev / args.steps) / 1e12
+    workload = "gemm_bias_gelu_tanh_4096x4096x4096_bf16"
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) / N(0,1/sqrt(K)))",
+        "config": {"workload": workload, "M": M, "N": N, "K": K, "op": "gemm+bias+gelu_tanh",
+                   "tile": desc.format_config(cfg), "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16, 4), "traffic": _load_traffic(workload),
+                     "kernel_us": round(ev / args.steps * 1e6, 2)},
+    }
+    if tuned is not None:  # noqa: SIM102
+        out["tuner"] = {"time_to_best_s": round(tuned.time_to_best_s, 3), "prune_rank_s": round(tuned.prune_rank_s, 4),
+                        "compile_s": round(tuned.compile_s, 4), "bench_s": round(tuned.bench_s, 3),
+                        "formula_top1": desc.format_config(tuned.formula_top1),
+                        "formula_top1_ms": round(tuned.formula_top1_ms, 5), "select_best_s": round(select_s, 4)}
+    del A, B, bias, C, d
+    torch.cuda.empty_cache()
+    if not args.no_ops and not args.headline_only_kernel:
+        out["ops"] = bench_ops(args.quick)
+    if not args.no_cpu and not args.headline_only_kernel:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -8,8 +8,9 @@
 // the HWIO filter viewed as [KH*KW*C, F]).
 //
 // Data path per K tile (BK):
-//   global --(buffer_load_dwordx4, 16 B per lane, OOB lanes read 0)--> VGPR staging
-//   --> LDS (XOR-swizzled 16 B chunks, STAGES buffers)
+//   global --(buffer_load_dwordx4 ... lds: 16 B per lane straight into LDS,
+//             range-checked so out-of-range lanes deliver 0)--> LDS ring of
+//             STAGES buffers holding XOR-swizzled 16 B chunks
 //   --> A fragments with ds_read_b128 (K contiguous per lane)
 //   --> B fragments with ds_read_b64_tr_b16 / ds_read_b64_tr_b8, which transpose
 //       the N-contiguous tile into the K-contiguous per-lane MFMA operand
@@ -21,7 +22,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace icpp {
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 enum DType { DT_F16 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_F32 = 3 };
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3 };
@@ -130,6 +143,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
+// 16-byte buffer load written straight to LDS (gfx950 LDS DMA): lane l of the
+// wave stores to lds_wave_base + 16*l.  lds_wave_base must be wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char ICPP_LDS* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (void ICPP_LDS*)lds_wave_base, 16, voff, soff, 0, 0);
+}
+// s_waitcnt vmcnt(N) leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 __device__ __forceinline__ void lds_store16(char ICPP_LDS* base, uint32_t off, i32x4 v) {
   *reinterpret_cast<i32x4 ICPP_LDS*>(base + off) = v;
 }
@@ -166,6 +190,11 @@ template <> struct Vec4Store<_Float16> {
     h4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
     *reinterpret_cast<h4*>(p) = h;
   }
+  static __device__ __forceinline__ void st_lds(char ICPP_LDS* p, f32x4 v) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    *reinterpret_cast<h4 ICPP_LDS*>(p) = h;
+  }
   static __device__ __forceinline__ f32x4 ld(const void* p) {
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     h4 h = *reinterpret_cast<const h4*>(p);
@@ -178,6 +207,11 @@ template <> struct Vec4Store<__bf16> {
     b4 h = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
     *reinterpret_cast<b4*>(p) = h;
   }
+  static __device__ __forceinline__ void st_lds(char ICPP_LDS* p, f32x4 v) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    b4 h = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+    *reinterpret_cast<b4 ICPP_LDS*>(p) = h;
+  }
   static __device__ __forceinline__ f32x4 ld(const void* p) {
     typedef __bf16 b4 __attribute__((ext_vector_type(4)));
     b4 h = *reinterpret_cast<const b4*>(p);
@@ -186,6 +220,7 @@ template <> struct Vec4Store<__bf16> {
 };
 template <> struct Vec4Store<float> {
   static __device__ __forceinline__ void st(void* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+  static __device__ __forceinline__ void st_lds(char ICPP_LDS* p, f32x4 v) { *reinterpret_cast<f32x4 ICPP_LDS*>(p) = v; }
   static __device__ __forceinline__ f32x4 ld(const void* p) { return *reinterpret_cast<const f32x4*>(p); }
 };
 
@@ -212,8 +247,11 @@ struct Tile {
   static constexpr int A_BYTES = BM * ROWB_A, B_BYTES = BK * ROWB_B;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int LDS_BYTES = STAGE_BYTES * STAGES;
-  static constexpr int RPB_A = (ROWB_A >= 128) ? 1 : (128 / ROWB_A);
-  static constexpr int SWZ_A = (CPR_A < 8) ? CPR_A : 8;
+  // LDS bank geometry (gfx950): 64 banks x 4 B; a ds_read_b128 services 16
+  // lanes per cycle, a ds_read_b64_tr_b{16,8} 32 lanes per cycle.  The XOR
+  // swizzles below make every such lane group touch 256 distinct bytes.
+  static constexpr int RPB_A = (ROWB_A >= 256) ? 1 : (256 / ROWB_A);  // A rows per 256-byte bank window
+  static constexpr int SWZ_A = (CPR_A < 16) ? CPR_A : 16;
 
   static_assert(WTM % MF == 0 && WTN % MF == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(BK % KI == 0, "BK must be a multiple of the MFMA K");
@@ -221,16 +259,42 @@ struct Tile {
   static_assert(CPR_A >= 2, "A rows must span >= 2 chunks");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS overflow");
 
+  static_assert(A_CHUNKS % 64 == 0 && B_CHUNKS % 64 == 0, "tile loads must cover whole waves");
+  static_assert(STAGES == 2 || (A_EVEN && B_EVEN), "deeper LDS rings need every thread to issue every load");
+  static_assert((SA + SB) * (STAGES > 2 ? STAGES - 2 : 0) < 64, "vmcnt range");
+
   // A: row r, logical 16 B chunk c -> byte offset in the A region
+  static __device__ __forceinline__ int a_swz(int r) { return (r / RPB_A) % SWZ_A; }
   static __device__ __forceinline__ uint32_t a_off(int r, int c) {
-    return (uint32_t)(r * ROWB_A + ((c ^ ((r / RPB_A) % SWZ_A)) << 4));
+    return (uint32_t)(r * ROWB_A + ((c ^ a_swz(r)) << 4));
   }
+  // B: XOR applied to the 16-byte chunk index of row k.  A transpose read
+  // covers 4 rows (b16) / 8 rows (b8) per 16 lanes; the second 16 lanes of the
+  // cycle either read the same rows at the next 16 columns (32x32 MFMA) or rows
+  // +8 (b16, 16x16) / +32 (b8, 16x16).  The chosen bits of k separate all of
+  // them into distinct bank slots; only bits that are constant per lane over
+  // the K steps are used, so addresses stay base + immediate.
+  static __device__ __forceinline__ int b_swz(int k) {
+    constexpr bool WIDE = ROWB_B >= 256;
+    if constexpr (ESZ == 2) {
+      if constexpr (MF == 16)
+        return WIDE ? (((k & 3) << 1) | (((k >> 3) & 1) << 3)) : ((((k >> 1) & 1) << 1) | (((k >> 3) & 1) << 2));
+      else
+        return WIDE ? ((k & 3) << 2) : (((k >> 1) & 1) << 2);
+    } else {
+      if constexpr (MF == 16)
+        return WIDE ? ((k & 7) | (((k >> 5) & 1) << 3)) : (((k >> 1) & 3) | (((k >> 5) & 1) << 2));
+      else
+        return WIDE ? ((k & 7) << 1) : (((k >> 1) & 3) << 1);
+    }
+  }
+  // rows after which b_swz repeats
+  static constexpr int B_SWZ_PERIOD = (ESZ == 1 && MF == 16) ? 64 : 16;
   // B: row k, logical chunk c -> byte offset in the B region. The XOR keeps the
   // rows that one transpose read touches together in distinct bank groups
   // (4 rows x 32 B for b16, 8 rows x 16 B for b8).
   static __device__ __forceinline__ uint32_t b_off(int k, int c) {
-    const int s = (ESZ == 2) ? ((k & 3) << 1) : (k & 7);
-    return (uint32_t)(k * ROWB_B + ((c ^ s) << 4));
+    return (uint32_t)(k * ROWB_B + ((c ^ b_swz(k)) << 4));
   }
 };
 
@@ -248,8 +312,20 @@ gemm_kernel(KArgs p) {
   typedef typename DTraits<DT>::BiasT BiasT;
   constexpr int ESZ = G::ESZ;
 
-  __shared__ __attribute__((aligned(16))) char smem_raw[G::LDS_BYTES];
-  char ICPP_LDS* smem = (char ICPP_LDS*)smem_raw;
+  // One LDS array per pipeline stage: distinct objects let the compiler see that
+  // the DMA writes into one stage never alias the fragment reads of another, so
+  // it does not serialise them with a vmcnt(0) wait.
+  __shared__ __attribute__((aligned(16))) char lds0[G::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char lds1[STAGES > 1 ? G::STAGE_BYTES : 16];
+  __shared__ __attribute__((aligned(16))) char lds2[STAGES > 2 ? G::STAGE_BYTES : 16];
+  __shared__ __attribute__((aligned(16))) char lds3[STAGES > 3 ? G::STAGE_BYTES : 16];
+  auto stage_base = [&](auto S) -> char ICPP_LDS* {
+    constexpr int s = decltype(S)::value;
+    if constexpr (s == 0) return (char ICPP_LDS*)lds0;
+    else if constexpr (s == 1) return (char ICPP_LDS*)lds1;
+    else if constexpr (s == 2) return (char ICPP_LDS*)lds2;
+    else return (char ICPP_LDS*)lds3;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -274,31 +350,44 @@ gemm_kernel(KArgs p) {
   const int k_len = min(p.k_split, p.K - k_begin);
   const int nk = k_len / BK;
 
-  // ---- global sources (raw buffer resources; out-of-range lanes read zeros) ----
+  // ---- global -> LDS: buffer_load_dwordx4 ... lds (16 B per lane, range-checked:
+  // out-of-range lanes deliver zeros).  Load i of wave w writes LDS chunks
+  // q = i*THREADS + w*64 + lane; each lane fetches the logical chunk that the
+  // XOR swizzle places in that slot, so the LDS image is the swizzled tile.
+  // When THREADS is a multiple of the chunks per row (and of the swizzle
+  // period), load i only moves the lane down by a fixed number of rows, so the
+  // per-load part of the address is a wave-uniform scalar (soffset) and one
+  // VGPR per operand suffices.
   const char* Ab = (const char*)p.A;
   const char* Bb = (const char*)p.B;
   __amdgpu_buffer_rsrc_t ra, rb;
-  uint32_t a_row_off[G::SA];
-  int a_chunk[G::SA];
-  // conv gather state
-  int a_img[ALOAD == A_IM2COL ? G::SA : 1], a_ih0[ALOAD == A_IM2COL ? G::SA : 1], a_iw0[ALOAD == A_IM2COL ? G::SA : 1];
   if constexpr (ALOAD == A_DENSE) {
     const uint64_t rem = (uint64_t)(p.M > row0 ? p.M - row0 : 0) * (uint64_t)p.lda * ESZ;
     ra = make_rsrc(Ab + (size_t)row0 * p.lda * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
-#pragma unroll
-    for (int i = 0; i < G::SA; ++i) {
-      const int q = tid + i * G::THREADS;
-      const int r = q / G::CPR_A;
-      a_chunk[i] = q % G::CPR_A;
-      a_row_off[i] = (uint32_t)(r * p.lda * ESZ + k_begin * ESZ + a_chunk[i] * 16);
-    }
   } else {
     ra = make_rsrc(Ab, (uint32_t)p.a_bytes_total);
+  }
+  {
+    const uint64_t rem = ((uint64_t)(p.K - 1) * p.ldb + (uint64_t)(p.N - col0)) * ESZ;
+    rb = make_rsrc(Bb + (size_t)col0 * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
+  }
+  constexpr bool A_UNIFORM = (ALOAD == A_DENSE) && (G::THREADS % G::CPR_A == 0) &&
+                             ((G::THREADS / G::CPR_A) % (G::RPB_A * G::SWZ_A) == 0);
+  constexpr bool B_UNIFORM = (G::THREADS % G::CPR_B == 0) && ((G::THREADS / G::CPR_B) % G::B_SWZ_PERIOD == 0);
+  constexpr int NA = A_UNIFORM ? 1 : G::SA;
+  constexpr int NB = B_UNIFORM ? 1 : G::SB;
+  uint32_t a_goff[NA];
+  int a_lc[ALOAD == A_IM2COL ? G::SA : 1];
+  int a_img[ALOAD == A_IM2COL ? G::SA : 1], a_ih0[ALOAD == A_IM2COL ? G::SA : 1], a_iw0[ALOAD == A_IM2COL ? G::SA : 1];
 #pragma unroll
-    for (int i = 0; i < G::SA; ++i) {
-      const int q = tid + i * G::THREADS;
-      const int r = q / G::CPR_A;
-      a_chunk[i] = q % G::CPR_A;
+  for (int i = 0; i < NA; ++i) {
+    const int q = tid + i * G::THREADS;
+    const int r = q / G::CPR_A;
+    const int c = (q % G::CPR_A) ^ G::a_swz(r);
+    if constexpr (ALOAD == A_DENSE) {
+      a_goff[i] = (uint32_t)(r * p.lda * ESZ + (k_begin + c * G::CH) * ESZ);
+    } else {
+      a_lc[i] = c;
       const int m = row0 + r;
       const int ohw = p.cOH * p.cOW;
       const int img = m / ohw;
@@ -307,34 +396,40 @@ gemm_kernel(KArgs p) {
       a_img[i] = (m < p.M) ? img : -1;
       a_ih0[i] = oh * p.cS - p.cP;
       a_iw0[i] = ow * p.cS - p.cP;
-      a_row_off[i] = 0;
+      a_goff[i] = 0;
     }
   }
-  {
-    const uint64_t rem = ((uint64_t)(p.K - 1) * p.ldb + (uint64_t)(p.N - col0)) * ESZ;
-    rb = make_rsrc(Bb + (size_t)col0 * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
-  }
-  uint32_t b_off_g[G::SB];
+  uint32_t b_goff[NB];
 #pragma unroll
-  for (int i = 0; i < G::SB; ++i) {
+  for (int i = 0; i < NB; ++i) {
     const int q = tid + i * G::THREADS;
-    const int k = q / G::CPR_B, c = q % G::CPR_B;
-    b_off_g[i] = (uint32_t)((k_begin + k) * p.ldb * ESZ + c * 16);
+    const int k = q / G::CPR_B;
+    const int c = (q % G::CPR_B) ^ G::b_swz(k);
+    b_goff[i] = (uint32_t)((k_begin + k) * p.ldb * ESZ + c * 16);
   }
+  const uint32_t a_row_step = (uint32_t)((G::THREADS / G::CPR_A) * p.lda * ESZ);  // bytes per load (A_UNIFORM)
+  const uint32_t b_row_step = (uint32_t)((G::THREADS / G::CPR_B) * p.ldb * ESZ);  // bytes per load (B_UNIFORM)
+  // byte offset of this wave's lane 0 within one load (wave-uniform -> SGPR)
+  const int wave_slot = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 16;
 
-  i32x4 ra_st[G::SA], rb_st[G::SB];
-
-  auto load_tile = [&](int kt) {
+  auto issue_tile = [&](int kt, auto S) {
+    char ICPP_LDS* as = stage_base(S);
+    char ICPP_LDS* bs = as + G::A_BYTES;
     if constexpr (ALOAD == A_DENSE) {
 #pragma unroll
       for (int i = 0; i < G::SA; ++i)
-        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) ra_st[i] = buf_load16(ra, a_row_off[i] + (uint32_t)(kt * BK * ESZ));
+        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) {
+          if constexpr (A_UNIFORM)
+            dma16(ra, a_goff[0], (uint32_t)(kt * BK * ESZ) + i * a_row_step, as + i * G::THREADS * 16 + wave_slot);
+          else
+            dma16(ra, a_goff[i], (uint32_t)(kt * BK * ESZ), as + i * G::THREADS * 16 + wave_slot);
+        }
     } else {
       // K index of this chunk -> (kh, kw, c); one filter tap per chunk since C % 8 == 0
       const int kbase = k_begin + kt * BK;
 #pragma unroll
       for (int i = 0; i < G::SA; ++i) {
-        const int k = kbase + a_chunk[i] * G::CH;
+        const int k = kbase + a_lc[i] * G::CH;
         const int tap = k / p.cC;
         const int ci = k - tap * p.cC;
         const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
@@ -342,26 +437,17 @@ gemm_kernel(KArgs p) {
         const bool ok = a_img[i] >= 0 && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW && k < p.K;
         const uint32_t off = ok ? (uint32_t)((((a_img[i] * p.cH + ih) * p.cW + iw) * p.cC + ci) * ESZ)
                                 : (uint32_t)p.a_bytes_total;
-        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) ra_st[i] = buf_load16(ra, off);
+        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
       }
     }
 #pragma unroll
     for (int i = 0; i < G::SB; ++i)
-      if (G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS) rb_st[i] = buf_load16(rb, b_off_g[i] + (uint32_t)(kt * BK * p.ldb * ESZ));
-  };
-  auto store_tile = [&](int s) {
-    char ICPP_LDS* as = smem + s * G::STAGE_BYTES;
-    char ICPP_LDS* bs = as + G::A_BYTES;
-#pragma unroll
-    for (int i = 0; i < G::SA; ++i) {
-      const int q = tid + i * G::THREADS;
-      if (G::A_EVEN || q < G::A_CHUNKS) lds_store16(as, G::a_off(q / G::CPR_A, q % G::CPR_A), ra_st[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < G::SB; ++i) {
-      const int q = tid + i * G::THREADS;
-      if (G::B_EVEN || q < G::B_CHUNKS) lds_store16(bs, G::b_off(q / G::CPR_B, q % G::CPR_B), rb_st[i]);
-    }
+      if (G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS) {
+        if constexpr (B_UNIFORM)
+          dma16(rb, b_goff[0], (uint32_t)(kt * BK * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
+        else
+          dma16(rb, b_goff[i], (uint32_t)(kt * BK * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
+      }
   };
 
   Acc acc[G::TM][G::TN];
@@ -370,76 +456,138 @@ gemm_kernel(KArgs p) {
 #pragma unroll
     for (int j = 0; j < G::TN; ++j) acc[i][j] = Acc{};
 
-  // per-lane fragment addressing (constant over the K loop)
-  const int a_lrow = wm * G::WTM + (lane % MF);
-  const int a_kgrp = lane / MF;                            // 0..3 (MF16) / 0..1 (MF32)
-  // B transpose-read lane mapping (group of 16 lanes reads 4 rows x 16 cols (b16) or 8 rows x 16 cols (b8))
+  // ---- per-lane fragment addressing --------------------------------------
+  // The swizzle term of a lane is the same for every MFMA tile row (tm) and
+  // every K step row offset, so an address is (per-lane register) + (compile-
+  // time immediate): A needs one register per K step, B one per N tile.
+  constexpr int NKS = BK / G::KI;
   const int li = lane & 15;
+  const int a_lrow = wm * G::WTM + (lane % MF);
+  const int a_kgrp = lane / MF;                     // K slice of this lane: 0..3 (MF16) / 0..1 (MF32)
+  const int a_s = G::a_swz(a_lrow);
+  uint32_t a_addr[NKS][ESZ == 2 ? 1 : 2];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if constexpr (ESZ == 2) {
+      const int c = (ks * G::KI) / 8 + a_kgrp;
+      a_addr[ks][0] = (uint32_t)(a_lrow * G::ROWB_A + ((c ^ a_s) << 4));
+    } else {
+      const int c = (ks * G::KI) / 16 + a_kgrp * 2;
+      a_addr[ks][0] = (uint32_t)(a_lrow * G::ROWB_A + ((c ^ a_s) << 4));
+      a_addr[ks][1] = (uint32_t)(a_lrow * G::ROWB_A + (((c + 1) ^ a_s) << 4));
+    }
+  }
   const int b_ncol_base = wn * G::WTN + ((MF == 32) ? 16 * ((lane >> 4) & 1) : 0);
   const int b_kgrp = (MF == 32) ? (lane >> 5) : (lane >> 4);
+  uint32_t b_addr[G::TN];
+#pragma unroll
+  for (int tn = 0; tn < G::TN; ++tn) {
+    const int n0 = b_ncol_base + tn * MF;
+    if constexpr (ESZ == 2) {
+      // tr16: lane i of a 16-lane group points at row k0 + i/4, columns n0 + 4*(i%4) .. +3
+      const int k = b_kgrp * 8 + (li >> 2);
+      const int col = n0 + 4 * (li & 3);
+      b_addr[tn] = (uint32_t)(k * G::ROWB_B + (((col >> 3) ^ G::b_swz(k)) << 4) + (col & 7) * 2);
+    } else {
+      // tr8: lane i of a 16-lane group points at row k0 + i/2, columns n0 + 8*(i%2) .. +7
+      const int k = b_kgrp * 32 + (li >> 1);
+      const int col = n0 + 8 * (li & 1);
+      b_addr[tn] = (uint32_t)(k * G::ROWB_B + (((col >> 4) ^ G::b_swz(k)) << 4) + (col & 15));
+    }
+  }
 
-  auto compute = [&](int s) {
-    const char ICPP_LDS* as = smem + s * G::STAGE_BYTES;
-    const char ICPP_LDS* bs = as + G::A_BYTES;
+  auto load_frags = [&](const char ICPP_LDS* as, const char ICPP_LDS* bs, auto KS, Frag* af, Frag* bf) {
+    constexpr int ks = decltype(KS)::value;
 #pragma unroll
-    for (int ks = 0; ks < BK / G::KI; ++ks) {
-      Frag af[G::TM], bf[G::TN];
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm) {
-        const int r = a_lrow + tm * MF;
-        if constexpr (ESZ == 2) {
-          const int c = (ks * G::KI) / 8 + a_kgrp;
-          af[tm] = lds_load16(as, G::a_off(r, c));
-        } else {
-          const int c = (ks * G::KI) / 16 + a_kgrp * 2;
-          i32x4 lo = lds_load16(as, G::a_off(r, c));
-          i32x4 hi = lds_load16(as, G::a_off(r, c + 1));
-          af[tm] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+    for (int tm = 0; tm < G::TM; ++tm) {
+      const uint32_t row_off = (uint32_t)(tm * MF * G::ROWB_A);
+      if constexpr (ESZ == 2) {
+        af[tm] = lds_load16(as, a_addr[ks][0] + row_off);
+      } else {
+        i32x4 lo = lds_load16(as, a_addr[ks][0] + row_off);
+        i32x4 hi = lds_load16(as, a_addr[ks][1] + row_off);
+        af[tm] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
+    }
 #pragma unroll
-      for (int tn = 0; tn < G::TN; ++tn) {
-        const int n0 = b_ncol_base + tn * MF;
-        if constexpr (ESZ == 2) {
-          const int kb = ks * G::KI + b_kgrp * 8;
-          const int col = n0 + 4 * (li & 3);
-          const int c = col >> 3, within = (col & 7) * 2;
-          const int r0 = kb + (li >> 2), r1 = kb + 4 + (li >> 2);
-          i32x2 lo = lds_tr16(bs, G::b_off(r0, c) + within);
-          i32x2 hi = lds_tr16(bs, G::b_off(r1, c) + within);
-          bf[tn] = i32x4{lo[0], lo[1], hi[0], hi[1]};
-        } else {
-          const int kb = ks * G::KI + b_kgrp * 32;
-          const int col = n0 + 8 * (li & 1);
-          const int c = col >> 4, within = col & 15;
-          i32x2 v[4];
+    for (int tn = 0; tn < G::TN; ++tn) {
+      if constexpr (ESZ == 2) {
+        const uint32_t k_off = (uint32_t)(ks * G::KI * G::ROWB_B);
+        i32x2 lo = lds_tr16(bs, b_addr[tn] + k_off);
+        i32x2 hi = lds_tr16(bs, b_addr[tn] + k_off + 4 * G::ROWB_B);
+        bf[tn] = i32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        i32x2 v[4];
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) v[rr] = lds_tr8(bs, G::b_off(kb + 8 * rr + (li >> 1), c) + within);
-          bf[tn] = i32x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
-        }
+        for (int rr = 0; rr < 4; ++rr)
+          v[rr] = lds_tr8(bs, b_addr[tn] + (uint32_t)((ks * G::KI + 8 * rr) * G::ROWB_B));
+        bf[tn] = i32x8{v[0][0], v[0][1], v[1][0], v[1][1], v[2][0], v[2][1], v[3][0], v[3][1]};
       }
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm)
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn) acc[tm][tn] = Op::run(bf[tn], af[tm], acc[tm][tn]);
     }
   };
 
-  // ---- pipelined mainloop ----
-  if (nk > 0) {
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int it = 0; it < nk; ++it) {
-      const int cur = (STAGES == 2) ? (it & 1) : 0;
-      if (it + 1 < nk) load_tile(it + 1);
-      compute(cur);
-      if (it + 1 < nk) {
-        if constexpr (STAGES == 1) __syncthreads();
-        store_tile((STAGES == 2) ? (cur ^ 1) : 0);
-        __syncthreads();
+  // One K tile from LDS stage s; the fragments of step ks+1 are read while the
+  // MFMAs of step ks issue.
+  auto compute = [&](auto S) {
+    const char ICPP_LDS* as = stage_base(S);
+    const char ICPP_LDS* bs = as + G::A_BYTES;
+    Frag af[2][G::TM], bf[2][G::TN];
+    load_frags(as, bs, std::integral_constant<int, 0>{}, af[0], bf[0]);
+    static_for<NKS>([&](auto KS) {
+      constexpr int ks = decltype(KS)::value;
+      if constexpr (ks + 1 < NKS)
+        load_frags(as, bs, std::integral_constant<int, ks + 1>{}, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn) acc[tm][tn] = Op::run(bf[ks & 1][tn], af[ks & 1][tm], acc[tm][tn]);
+    });
+    // Issue order for the scheduler: the reads of step 0, then for every later
+    // step its reads spread evenly between the MFMAs of the step before (left
+    // alone, the backend re-reads fragments just before use and waits on each).
+    constexpr int DS_PER_KS = G::TM * (ESZ == 2 ? 1 : 2) + G::TN * (ESZ == 2 ? 2 : 4);
+    constexpr int MFMA_PER_KS = G::TM * G::TN;
+    __builtin_amdgcn_sched_group_barrier(0x100, DS_PER_KS, 0);
+    static_for<NKS>([&](auto KS) {
+      constexpr int ks = decltype(KS)::value;
+      if constexpr (ks + 1 < NKS) {
+        static_for<MFMA_PER_KS>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          constexpr int ds = (i + 1) * DS_PER_KS / MFMA_PER_KS - i * DS_PER_KS / MFMA_PER_KS;
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);
+        });
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, MFMA_PER_KS, 0);
       }
-    }
+    });
+  };
+
+  // ---- pipelined mainloop: STAGES-deep LDS ring, one barrier per K tile ----
+  // Tile kt+STAGES-1 is fetched into the stage that tile kt-1 used while tile kt
+  // is multiplied; the barrier at the top of iteration kt both publishes tile
+  // kt (after this wave's own loads for it completed) and retires stage kt-1.
+  constexpr int LOADS = G::SA + G::SB;  // loads per thread per tile (all threads: A_EVEN && B_EVEN for STAGES > 2)
+  static_for<STAGES - 1>([&](auto S) {
+    if (decltype(S)::value < nk) issue_tile(decltype(S)::value, S);
+  });
+  for (int kt0 = 0; kt0 < nk; kt0 += STAGES) {
+    // the stage index of each step is a compile-time constant: kt0 % STAGES == 0
+    static_for<STAGES>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int kt = kt0 + j;
+      if (kt < nk) {
+        if constexpr (STAGES > 2) {
+          if (nk - 1 - kt >= STAGES - 2) wait_vmcnt<(STAGES - 2) * LOADS>();
+          else wait_vmcnt<0>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        __syncthreads();
+        if (kt + STAGES - 1 < nk) issue_tile(kt + STAGES - 1, std::integral_constant<int, (j + STAGES - 1) % STAGES>{});
+        compute(J);
+      }
+    });
   }
 
   // ---- epilogue ----
@@ -451,6 +599,55 @@ gemm_kernel(KArgs p) {
   };
   auto get4 = [&](int tm, int tn, int g) {
     return f32x4{acc[tm][tn][4 * g + 0], acc[tm][tn][4 * g + 1], acc[tm][tn][4 * g + 2], acc[tm][tn][4 * g + 3]};
+  };
+
+  // Output through LDS: for each MFMA row band (tm) a wave writes its values
+  // (converted to OutT) into a private padded LDS region, then re-reads them as
+  // 16-byte row chunks, so global stores cover whole contiguous row segments
+  // instead of 8-byte pieces of 16 different rows.
+  auto store_staged = [&](auto&& value4) {
+    constexpr int OSZ = (int)sizeof(OutT);
+    constexpr int ROWB_O = G::WTN * OSZ + 16;           // +16 B rotates rows across banks
+    constexpr int REGION = MF * ROWB_O;
+    constexpr int CPR_O = G::WTN * OSZ / 16;             // 16-byte chunks per output row
+    constexpr int CHUNK_ELEMS = 16 / OSZ;
+    constexpr int PER_STAGE = G::STAGE_BYTES / REGION;  // wave regions per stage array
+    static_assert(PER_STAGE * STAGES >= WM * WN, "epilogue staging must fit the LDS stages");
+    static_assert((G::WTN * OSZ) % 16 == 0, "wave tile rows must be whole 16-byte chunks");
+    OutT* C = (OutT*)p.C;
+    const int w_arr = wave / PER_STAGE;
+    char ICPP_LDS* arr = (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
+                       : (w_arr == 2) ? (char ICPP_LDS*)lds2 : (char ICPP_LDS*)lds3;
+    char ICPP_LDS* region = arr + (wave % PER_STAGE) * REGION;
+    __syncthreads();  // every wave is done reading the pipeline stages
+#pragma unroll
+    for (int tm = 0; tm < G::TM; ++tm) {
+#pragma unroll
+      for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const f32x4 v = value4(tm, tn, g);
+          const int lcol = tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
+          Vec4Store<OutT>::st_lds(region + (lane % MF) * ROWB_O + lcol * OSZ, v);
+        }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int q0 = 0; q0 < MF * CPR_O; q0 += 64) {
+        const int q = q0 + lane;
+        if ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O) {
+          const int rr = q / CPR_O, cc = q % CPR_O;
+          const i32x4 v = *(const i32x4 ICPP_LDS*)(region + rr * ROWB_O + cc * 16);
+          const int m = row0 + wm * G::WTM + tm * MF + rr;
+          const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
+          if (m < p.M && n < p.N) *(i32x4*)(C + (size_t)m * p.ldc + n) = v;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
   };
 
   if constexpr (EPI == EPI_STORE) {
@@ -468,24 +665,21 @@ gemm_kernel(KArgs p) {
           }
       }
     } else {
-      OutT* C = (OutT*)p.C;
       const BiasT* bias = (const BiasT*)p.bias;
+      f32x4 bv[G::TN][NG];
 #pragma unroll
       for (int tn = 0; tn < G::TN; ++tn)
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           const int n = out_col(tn, g);
-          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-          if (bias != nullptr && n < p.N) bv = Vec4Store<BiasT>::ld(bias + n);
-#pragma unroll
-          for (int tm = 0; tm < G::TM; ++tm) {
-            const int m = out_row(tm);
-            f32x4 v = get4(tm, tn, g);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e] * p.alpha + bv[e], p.act);
-            if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
-          }
+          bv[tn][g] = (bias != nullptr && n < p.N) ? Vec4Store<BiasT>::ld(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
+      store_staged([&](int tm, int tn, int g) {
+        f32x4 v = get4(tm, tn, g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e] * p.alpha + bv[tn][g][e], p.act);
+        return v;
+      });
     }
   } else {
     // LayerNorm epilogues: x = acc + bias, statistics over valid columns (n < N)
@@ -560,7 +754,8 @@ gemm_kernel(KArgs p) {
       // EPI_LN_ROW: the workgroup owns whole rows (tiles_n == 1, N <= BN); two-pass
       // mean / centred variance in registers, cross-wave through LDS.
       __syncthreads();  // mainloop LDS no longer needed
-      float ICPP_LDS* red = (float ICPP_LDS*)smem;       // [WN][BM]
+      static_assert(2 * WN * BM * 4 <= G::STAGE_BYTES, "LN reduction scratch must fit one LDS stage");
+      float ICPP_LDS* red = (float ICPP_LDS*)lds0;       // [WN][BM]
       float ICPP_LDS* red2 = red + WN * BM;               // [WN][BM]
       const BiasT* gamma = (const BiasT*)p.gamma;
       const BiasT* beta = (const BiasT*)p.beta;

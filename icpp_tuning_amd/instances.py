@@ -50,6 +50,21 @@ class Inst:
         return 64 * self.wm * self.wn
 
     @property
+    def acc_regs(self) -> int:
+        """fp32 accumulator registers per lane."""
+        return self.bm * self.bn // self.threads
+
+    @property
+    def compile_flags(self) -> List[str]:
+        """Per-instance code-generation flags.  When the accumulators fit the
+        architectural VGPRs alongside the fragments, the MFMAs are told to read
+        and write VGPRs: otherwise the backend may keep the loop-carried
+        accumulators in VGPRs and copy them into AGPRs every iteration."""
+        if self.acc_regs <= 160:
+            return ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+        return []
+
+    @property
     def lds_bytes(self) -> int:
         e = ESZ[self.dtype]
         return (self.bm * self.bk + self.bk * self.bn) * e * self.stages
@@ -71,8 +86,10 @@ class Inst:
             problems.append("A rows shorter than 32 bytes")
         if self.lds_bytes > 160 * 1024:
             problems.append("LDS overflow")
-        if self.stages not in (1, 2):
-            problems.append("stages must be 1 or 2")
+        if self.stages not in (2, 3, 4):
+            problems.append("stages must be 2, 3 or 4")
+        if self.stages > 2 and ((self.bm * self.bk * e // 16) % self.threads or (self.bk * self.bn * e // 16) % self.threads):
+            problems.append("deeper LDS rings need the tile loads to divide evenly over the threads")
         if problems:
             raise ValueError(f"{self.name}: " + "; ".join(problems))
 
@@ -86,6 +103,11 @@ def _gemm_tiles(dtype: str) -> List[Inst]:
         _g(dtype, 256, 256, 64, 2, 2, 32),
         _g(dtype, 256, 256, 64, 2, 2, 16),
         _g(dtype, 256, 256, 64, 2, 4, 32),
+        _g(dtype, 256, 256, 64, 2, 4, 16),
+        _g(dtype, 256, 256, 32, 2, 4, 32, st=4),
+        _g(dtype, 256, 256, 32, 2, 2, 32, st=4),
+        _g(dtype, 256, 128, 64, 2, 2, 32, st=3),
+        _g(dtype, 128, 256, 64, 2, 2, 32, st=3),
         _g(dtype, 256, 128, 64, 2, 2, 32),
         _g(dtype, 128, 256, 64, 2, 2, 32),
         _g(dtype, 128, 128, 64, 2, 2, 32),
@@ -103,6 +125,8 @@ def _fp8_tiles() -> List[Inst]:
     d = "fp8"
     return [
         _g(d, 256, 256, 128, 2, 2, 32),
+        _g(d, 256, 256, 128, 2, 4, 32),
+        _g(d, 256, 256, 64, 2, 4, 32, st=4),
         _g(d, 256, 128, 128, 2, 2, 32),
         _g(d, 128, 128, 128, 2, 2, 32),
         _g(d, 128, 128, 128, 2, 2, 16),
