@@ -244,6 +244,7 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   a.tiles_n = ceil_div(F, t.block_n);
   a.cH = H; a.cW = W; a.cC = C; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH; a.cOW = OW;
   a.a_bytes_total = (uint32_t)xbytes;
+  a.tap_uniform = (C % t.block_k == 0) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(a.tiles_m * a.tiles_n, split_k);
   if (split_k > 1) {

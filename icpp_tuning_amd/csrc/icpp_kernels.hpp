@@ -51,6 +51,8 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 #define ICPP_LDS __attribute__((address_space(3)))
+// kernel-local lambdas must inline: an outlined one takes its captures through scratch memory
+#define ICPP_INLINE __attribute__((always_inline))
 #define ICPP_BUF_DWORD3 0x00020000  // gfx9 raw buffer: 32-bit data format, no swizzle
 
 // Kernel arguments (passed by value; everything the launcher resolved on the host).
@@ -74,6 +76,7 @@ struct KArgs {
   // implicit-GEMM conv geometry (A_IM2COL); GEMM M = Nb*OH*OW, K = KH*KW*C
   int cH, cW, cC, cKW, cS, cP, cD, cOH, cOW;
   uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
+  int tap_uniform;         // C % BK == 0: every K tile lies inside one filter tap
 };
 
 template <int DT> struct DTraits;
@@ -319,7 +322,7 @@ gemm_kernel(KArgs p) {
   __shared__ __attribute__((aligned(16))) char lds1[STAGES > 1 ? G::STAGE_BYTES : 16];
   __shared__ __attribute__((aligned(16))) char lds2[STAGES > 2 ? G::STAGE_BYTES : 16];
   __shared__ __attribute__((aligned(16))) char lds3[STAGES > 3 ? G::STAGE_BYTES : 16];
-  auto stage_base = [&](auto S) -> char ICPP_LDS* {
+  auto stage_base = [&](auto S) -> char ICPP_LDS* ICPP_INLINE {
     constexpr int s = decltype(S)::value;
     if constexpr (s == 0) return (char ICPP_LDS*)lds0;
     else if constexpr (s == 1) return (char ICPP_LDS*)lds1;
@@ -379,6 +382,7 @@ gemm_kernel(KArgs p) {
   uint32_t a_goff[NA];
   int a_lc[ALOAD == A_IM2COL ? G::SA : 1];
   int a_img[ALOAD == A_IM2COL ? G::SA : 1], a_ih0[ALOAD == A_IM2COL ? G::SA : 1], a_iw0[ALOAD == A_IM2COL ? G::SA : 1];
+  int a_pix[ALOAD == A_IM2COL ? G::SA : 1];  // NHWC pixel index of the (kh, kw) = (0, 0) tap
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int q = tid + i * G::THREADS;
@@ -396,6 +400,7 @@ gemm_kernel(KArgs p) {
       a_img[i] = (m < p.M) ? img : -1;
       a_ih0[i] = oh * p.cS - p.cP;
       a_iw0[i] = ow * p.cS - p.cP;
+      a_pix[i] = (img * p.cH + a_ih0[i]) * p.cW + a_iw0[i];
       a_goff[i] = 0;
     }
   }
@@ -412,7 +417,7 @@ gemm_kernel(KArgs p) {
   // byte offset of this wave's lane 0 within one load (wave-uniform -> SGPR)
   const int wave_slot = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 16;
 
-  auto issue_tile = [&](int kt, auto S) {
+  auto issue_tile = [&](int kt, auto S) ICPP_INLINE {
     char ICPP_LDS* as = stage_base(S);
     char ICPP_LDS* bs = as + G::A_BYTES;
     if constexpr (ALOAD == A_DENSE) {
@@ -424,6 +429,24 @@ gemm_kernel(KArgs p) {
           else
             dma16(ra, a_goff[i], (uint32_t)(kt * BK * ESZ), as + i * G::THREADS * 16 + wave_slot);
         }
+    } else if (p.tap_uniform) {
+      // The whole K tile is one filter tap (kh, kw) and channels c0 .. c0+BK-1:
+      // the tap decomposition is wave-uniform scalar work, each lane adds a
+      // constant pixel delta to its precomputed base and checks the padding.
+      const int kbase = k_begin + kt * BK;
+      const int tap = __builtin_amdgcn_readfirstlane(kbase / p.cC);
+      const int c0 = kbase - tap * p.cC;
+      const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
+      const int dh = kh * p.cD, dw = kw * p.cD;
+      const int pix_delta = dh * p.cW + dw;
+#pragma unroll
+      for (int i = 0; i < G::SA; ++i) {
+        const int ih = a_ih0[i] + dh, iw = a_iw0[i] + dw;
+        const bool ok = a_img[i] >= 0 && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW;
+        const uint32_t off = ok ? (uint32_t)(((a_pix[i] + pix_delta) * p.cC + c0 + a_lc[i] * G::CH) * ESZ)
+                                : (uint32_t)p.a_bytes_total;
+        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
+      }
     } else {
       // K index of this chunk -> (kh, kw, c); one filter tap per chunk since C % 8 == 0
       const int kbase = k_begin + kt * BK;
@@ -496,7 +519,7 @@ gemm_kernel(KArgs p) {
     }
   }
 
-  auto load_frags = [&](const char ICPP_LDS* as, const char ICPP_LDS* bs, auto KS, Frag* af, Frag* bf) {
+  auto load_frags = [&](const char ICPP_LDS* as, const char ICPP_LDS* bs, auto KS, Frag* af, Frag* bf) ICPP_INLINE {
     constexpr int ks = decltype(KS)::value;
 #pragma unroll
     for (int tm = 0; tm < G::TM; ++tm) {
@@ -528,12 +551,12 @@ gemm_kernel(KArgs p) {
 
   // One K tile from LDS stage s; the fragments of step ks+1 are read while the
   // MFMAs of step ks issue.
-  auto compute = [&](auto S) {
+  auto compute = [&](auto S) ICPP_INLINE {
     const char ICPP_LDS* as = stage_base(S);
     const char ICPP_LDS* bs = as + G::A_BYTES;
     Frag af[2][G::TM], bf[2][G::TN];
     load_frags(as, bs, std::integral_constant<int, 0>{}, af[0], bf[0]);
-    static_for<NKS>([&](auto KS) {
+    static_for<NKS>([&](auto KS) ICPP_INLINE {
       constexpr int ks = decltype(KS)::value;
       if constexpr (ks + 1 < NKS)
         load_frags(as, bs, std::integral_constant<int, ks + 1>{}, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
@@ -548,10 +571,10 @@ gemm_kernel(KArgs p) {
     constexpr int DS_PER_KS = G::TM * (ESZ == 2 ? 1 : 2) + G::TN * (ESZ == 2 ? 2 : 4);
     constexpr int MFMA_PER_KS = G::TM * G::TN;
     __builtin_amdgcn_sched_group_barrier(0x100, DS_PER_KS, 0);
-    static_for<NKS>([&](auto KS) {
+    static_for<NKS>([&](auto KS) ICPP_INLINE {
       constexpr int ks = decltype(KS)::value;
       if constexpr (ks + 1 < NKS) {
-        static_for<MFMA_PER_KS>([&](auto I) {
+        static_for<MFMA_PER_KS>([&](auto I) ICPP_INLINE {
           constexpr int i = decltype(I)::value;
           constexpr int ds = (i + 1) * DS_PER_KS / MFMA_PER_KS - i * DS_PER_KS / MFMA_PER_KS;
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -568,12 +591,12 @@ gemm_kernel(KArgs p) {
   // is multiplied; the barrier at the top of iteration kt both publishes tile
   // kt (after this wave's own loads for it completed) and retires stage kt-1.
   constexpr int LOADS = G::SA + G::SB;  // loads per thread per tile (all threads: A_EVEN && B_EVEN for STAGES > 2)
-  static_for<STAGES - 1>([&](auto S) {
+  static_for<STAGES - 1>([&](auto S) ICPP_INLINE {
     if (decltype(S)::value < nk) issue_tile(decltype(S)::value, S);
   });
   for (int kt0 = 0; kt0 < nk; kt0 += STAGES) {
     // the stage index of each step is a compile-time constant: kt0 % STAGES == 0
-    static_for<STAGES>([&](auto J) {
+    static_for<STAGES>([&](auto J) ICPP_INLINE {
       constexpr int j = decltype(J)::value;
       const int kt = kt0 + j;
       if (kt < nk) {
@@ -593,11 +616,11 @@ gemm_kernel(KArgs p) {
   // ---- epilogue ----
   // lane owns output row (lane % MF) of each MFMA tile and groups of 4 consecutive columns
   constexpr int NG = Op::ACC / 4;  // column groups per MFMA tile
-  auto out_row = [&](int tm) { return row0 + wm * G::WTM + tm * MF + (lane % MF); };
-  auto out_col = [&](int tn, int g) {
+  auto out_row = [&](int tm) ICPP_INLINE { return row0 + wm * G::WTM + tm * MF + (lane % MF); };
+  auto out_col = [&](int tn, int g) ICPP_INLINE {
     return col0 + wn * G::WTN + tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
   };
-  auto get4 = [&](int tm, int tn, int g) {
+  auto get4 = [&](int tm, int tn, int g) ICPP_INLINE {
     return f32x4{acc[tm][tn][4 * g + 0], acc[tm][tn][4 * g + 1], acc[tm][tn][4 * g + 2], acc[tm][tn][4 * g + 3]};
   };
 
@@ -605,7 +628,7 @@ gemm_kernel(KArgs p) {
   // (converted to OutT) into a private padded LDS region, then re-reads them as
   // 16-byte row chunks, so global stores cover whole contiguous row segments
   // instead of 8-byte pieces of 16 different rows.
-  auto store_staged = [&](auto&& value4) {
+  auto store_staged = [&](auto&& value4) ICPP_INLINE {
     constexpr int OSZ = (int)sizeof(OutT);
     constexpr int ROWB_O = G::WTN * OSZ + 16;           // +16 B rotates rows across banks
     constexpr int REGION = MF * ROWB_O;
@@ -700,7 +723,7 @@ gemm_kernel(KArgs p) {
           for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] = ok ? (acc[tm][tn][4 * g + e] + bv[e]) : 0.f;
       }
     // row sums over this wave's columns, reduced across the lanes sharing a row
-    auto lane_reduce = [&](float v) {
+    auto lane_reduce = [&](float v) ICPP_INLINE {
       if (MF == 16) {
         v += __shfl_xor(v, 16);
         v += __shfl_xor(v, 32);

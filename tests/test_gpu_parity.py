@@ -190,3 +190,27 @@ def test_config5_fp8(gpu, M, NK):
     y = k(d["A"].cuda(), d["B"].cuda(), d["scale_a"], d["scale_b"], d["bias"].cuda())
     torch.cuda.synchronize()
     _close(y, ref, 1e-2, 1e-2, f"config5 M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("geom", [
+    # (N, H, W, C, F, KH, KW, stride, pad, dilation)
+    (2, 7, 6, 16, 64, 2, 2, 1, 0, 1),    # K tile spans 4 filter taps (general gather path)
+    (2, 9, 9, 64, 64, 3, 3, 2, 1, 1),    # stride 2
+    (2, 8, 8, 64, 128, 3, 3, 1, 2, 2),   # dilation 2
+    (1, 5, 5, 128, 72, 1, 1, 1, 0, 1),   # 1x1, F not a multiple of the tile
+])
+def test_conv_geometries(gpu, geom):
+    Nb, H, W, C, F, KH, KW, S, P, D = geom
+    d = I.config4(Nb, H, W, C, F, KH, KW)
+    ref = O.conv2d_nhwc_ref(d["X"], d["W"], S, P, D)
+    X, Wt = d["X"].cuda(), d["W"].cuda()
+    for idx, inst in enumerate(family_instances("conv2d")):
+        if (KH * KW * C) % inst.bk:
+            continue
+        raw = raw_from_inst(inst, 1)
+        print(f"[parity] conv {geom} {inst.name}", flush=True)
+        k = conv_mod.build_conv2d_kernel(Nb, C, H, W, F, KH, KW, S, P, D, config=raw)
+        Y = torch.full(tuple(ref.shape), float("nan"), dtype=torch.float16, device="cuda")
+        k(X, Wt, Y)
+        torch.cuda.synchronize()
+        _close(Y, ref, 1e-2, 1e-2, f"conv {geom} {inst.name}")
