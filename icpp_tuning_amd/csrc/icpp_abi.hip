@@ -149,8 +149,9 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
     return fail(ICPP_E_SHAPE, "icpp_gemm: K=%d not a multiple of block_k*split_k=%d", K, t.block_k * split_k);
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias)))
     return fail(ICPP_E_ARG, "icpp_gemm: pointers must be 16-byte aligned");
-  if ((uint64_t)t.block_m * lda * e > 0x7FFFFFFFull || (uint64_t)K * ldb * e > 0xFFFFFFF0ull)
-    return fail(ICPP_E_SHAPE, "icpp_gemm: operand exceeds the 4 GiB buffer range");
+  if ((uint64_t)t.block_m * lda * e > 0x7FFFFFFFull || (uint64_t)K * ldb * e > 0xFFFFFFF0ull ||
+      (uint64_t)t.block_m * ldc * 2 > 0x7FFFFFFFull)
+    return fail(ICPP_E_SHAPE, "icpp_gemm: operand exceeds the buffer range (block rows of A / C < 2 GiB, B < 4 GiB)");
   KArgs a = base_args();
   a.A = A; a.B = B; a.bias = bias; a.C = C;
   a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
@@ -234,7 +235,9 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   if (Mg > 0x7FFFFFFF || Kg % ((long long)t.block_k * split_k))
     return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: K=%lld not a multiple of block_k*split_k=%d", Kg, t.block_k * split_k);
   const unsigned long long xbytes = (unsigned long long)N * H * W * C * 2;
-  if (xbytes > 0xFFFFFFF0ull) return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: input exceeds the 4 GiB buffer range");
+  // padding taps load from offset xbytes (past the range): keep it and the output block rows below 2 GiB
+  if (xbytes > 0x7FFFFFF0ull || (uint64_t)t.block_m * F * 2 > 0x7FFFFFFFull)
+    return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: input or output exceeds the 2 GiB buffer range");
   if (!aligned16(X) || !aligned16(Wt) || !aligned16(Y)) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: pointers must be 16-byte aligned");
   KArgs a = base_args();
   a.A = X; a.B = Wt; a.C = Y;

@@ -157,6 +157,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+// Workgroup barrier for the LDS ring.  __syncthreads() carries a workgroup
+// release fence, which must cover outstanding LDS-DMA writes and so waits for
+// vmcnt(0): every barrier would drain all prefetched tiles and a deeper ring
+// would buy nothing.  Here each wave has already waited (vmcnt) for its own
+// loads of the tile being published, and its fragment reads of the retired
+// stage were consumed by MFMAs, so a plain s_barrier suffices; the asm memory
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 __device__ __forceinline__ void lds_store16(char ICPP_LDS* base, uint32_t off, i32x4 v) {
   *reinterpret_cast<i32x4 ICPP_LDS*>(base + off) = v;
 }
@@ -171,17 +181,36 @@ __device__ __forceinline__ i32x2 lds_tr8(const char ICPP_LDS* base, uint32_t off
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((i32x2 ICPP_LDS*)(base + off));
 }
 
-// Epilogue activation, branch-free so the unrolled epilogue stays small enough
-// for the accumulators to remain in registers:
+// Epilogue activations, resolved at compile time (the epilogue is instantiated
+// once per activation and picked with one uniform switch per tile):
 //   GELU-tanh(x) = 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
 //   SiLU(x)      = x * sigmoid(x)
-__device__ __forceinline__ float apply_act(float x, int act) {
-  const float u2 = 1.5957691216057308f * (x + 0.044715f * x * x * x);
-  const float z = (act == ACT_GELU_TANH) ? u2 : x;
-  const float sg = 1.f / (1.f + __expf(-z));
-  const float r = (act >= ACT_GELU_TANH) ? x * sg : x;
-  return (act == ACT_RELU) ? fmaxf(x, 0.f) : r;
+// sigmoid(z) = 1 / (1 + exp(-z)) with the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32: ~1 ulp each) instead of an IEEE division; z -> -inf
+// gives rcp(inf) = 0, so x * sigmoid stays finite.
+__device__ __forceinline__ float fast_sigmoid(float z) { return __builtin_amdgcn_rcpf(1.f + __expf(-z)); }
+template <int ACT>
+__device__ __forceinline__ float act_fn(float x) {
+  if constexpr (ACT == ACT_RELU) return fmaxf(x, 0.f);
+  else if constexpr (ACT == ACT_GELU_TANH) return x * fast_sigmoid(1.5957691216057308f * (x + 0.044715f * x * x * x));
+  else if constexpr (ACT == ACT_SILU) return x * fast_sigmoid(x);
+  else return x;
 }
+// f(std::integral_constant<int, act>) for the runtime activation code act
+template <typename F>
+__device__ __forceinline__ void dispatch_act(int act, F&& f) {
+  switch (act) {
+    case ACT_RELU: f(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_GELU_TANH: f(std::integral_constant<int, ACT_GELU_TANH>{}); break;
+    case ACT_SILU: f(std::integral_constant<int, ACT_SILU>{}); break;
+    default: f(std::integral_constant<int, ACT_NONE>{}); break;
+  }
+}
+// 16-byte buffer store; offsets >= the descriptor's range are dropped by the hardware
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
+#define ICPP_OOB_OFFSET 0x80000000u  // past every store descriptor (ranges are < 2 GiB)
 
 template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
@@ -417,42 +446,39 @@ gemm_kernel(KArgs p) {
   // byte offset of this wave's lane 0 within one load (wave-uniform -> SGPR)
   const int wave_slot = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 16;
 
-  auto issue_tile = [&](int kt, auto S) ICPP_INLINE {
+  // One 16-byte-per-lane load of tile kt into stage S: loads 0 .. SA-1 move A
+  // chunks, SA .. SA+SB-1 move B chunks.  Issued one at a time so the mainloop
+  // can spread them between the MFMAs of the tile being multiplied.
+  auto issue_load = [&](int kt, auto S, auto L) ICPP_INLINE {
+    constexpr int l = decltype(L)::value;
     char ICPP_LDS* as = stage_base(S);
     char ICPP_LDS* bs = as + G::A_BYTES;
-    if constexpr (ALOAD == A_DENSE) {
-#pragma unroll
-      for (int i = 0; i < G::SA; ++i)
-        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) {
-          if constexpr (A_UNIFORM)
-            dma16(ra, a_goff[0], (uint32_t)(kt * BK * ESZ) + i * a_row_step, as + i * G::THREADS * 16 + wave_slot);
-          else
-            dma16(ra, a_goff[i], (uint32_t)(kt * BK * ESZ), as + i * G::THREADS * 16 + wave_slot);
-        }
-    } else if (p.tap_uniform) {
-      // The whole K tile is one filter tap (kh, kw) and channels c0 .. c0+BK-1:
-      // the tap decomposition is wave-uniform scalar work, each lane adds a
-      // constant pixel delta to its precomputed base and checks the padding.
-      const int kbase = k_begin + kt * BK;
-      const int tap = __builtin_amdgcn_readfirstlane(kbase / p.cC);
-      const int c0 = kbase - tap * p.cC;
-      const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
-      const int dh = kh * p.cD, dw = kw * p.cD;
-      const int pix_delta = dh * p.cW + dw;
-#pragma unroll
-      for (int i = 0; i < G::SA; ++i) {
+    if constexpr (l < G::SA) {
+      constexpr int i = l;
+      if (!(G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS)) return;
+      if constexpr (ALOAD == A_DENSE) {
+        if constexpr (A_UNIFORM)
+          dma16(ra, a_goff[0], (uint32_t)(kt * BK * ESZ) + i * a_row_step, as + i * G::THREADS * 16 + wave_slot);
+        else
+          dma16(ra, a_goff[i], (uint32_t)(kt * BK * ESZ), as + i * G::THREADS * 16 + wave_slot);
+      } else if (p.tap_uniform) {
+        // The whole K tile is one filter tap (kh, kw) and channels c0 .. c0+BK-1:
+        // the tap decomposition is wave-uniform scalar work, each lane adds a
+        // constant pixel delta to its precomputed base and checks the padding.
+        const int kbase = k_begin + kt * BK;
+        const int tap = __builtin_amdgcn_readfirstlane(kbase / p.cC);
+        const int c0 = kbase - tap * p.cC;
+        const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
+        const int dh = kh * p.cD, dw = kw * p.cD;
+        const int pix_delta = dh * p.cW + dw;
         const int ih = a_ih0[i] + dh, iw = a_iw0[i] + dw;
         const bool ok = a_img[i] >= 0 && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW;
         const uint32_t off = ok ? (uint32_t)(((a_pix[i] + pix_delta) * p.cC + c0 + a_lc[i] * G::CH) * ESZ)
                                 : (uint32_t)p.a_bytes_total;
-        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
-      }
-    } else {
-      // K index of this chunk -> (kh, kw, c); one filter tap per chunk since C % 8 == 0
-      const int kbase = k_begin + kt * BK;
-#pragma unroll
-      for (int i = 0; i < G::SA; ++i) {
-        const int k = kbase + a_lc[i] * G::CH;
+        dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
+      } else {
+        // K index of this chunk -> (kh, kw, c); one filter tap per chunk since C % 8 == 0
+        const int k = k_begin + kt * BK + a_lc[i] * G::CH;
         const int tap = k / p.cC;
         const int ci = k - tap * p.cC;
         const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
@@ -460,17 +486,20 @@ gemm_kernel(KArgs p) {
         const bool ok = a_img[i] >= 0 && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW && k < p.K;
         const uint32_t off = ok ? (uint32_t)((((a_img[i] * p.cH + ih) * p.cW + iw) * p.cC + ci) * ESZ)
                                 : (uint32_t)p.a_bytes_total;
-        if (G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS) dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
+        dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
       }
+    } else {
+      constexpr int i = l - G::SA;
+      if (!(G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS)) return;
+      if constexpr (B_UNIFORM)
+        dma16(rb, b_goff[0], (uint32_t)(kt * BK * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
+      else
+        dma16(rb, b_goff[i], (uint32_t)(kt * BK * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
     }
-#pragma unroll
-    for (int i = 0; i < G::SB; ++i)
-      if (G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS) {
-        if constexpr (B_UNIFORM)
-          dma16(rb, b_goff[0], (uint32_t)(kt * BK * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
-        else
-          dma16(rb, b_goff[i], (uint32_t)(kt * BK * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
-      }
+  };
+  constexpr int LOADS = G::SA + G::SB;  // loads per thread per tile
+  auto issue_tile = [&](int kt, auto S) ICPP_INLINE {
+    static_for<LOADS>([&](auto L) ICPP_INLINE { issue_load(kt, S, L); });
   };
 
   Acc acc[G::TM][G::TN];
@@ -549,69 +578,89 @@ gemm_kernel(KArgs p) {
     }
   };
 
-  // One K tile from LDS stage s; the fragments of step ks+1 are read while the
-  // MFMAs of step ks issue.
-  auto compute = [&](auto S) ICPP_INLINE {
-    const char ICPP_LDS* as = stage_base(S);
-    const char ICPP_LDS* bs = as + G::A_BYTES;
-    Frag af[2][G::TM], bf[2][G::TN];
-    load_frags(as, bs, std::integral_constant<int, 0>{}, af[0], bf[0]);
-    static_for<NKS>([&](auto KS) ICPP_INLINE {
-      constexpr int ks = decltype(KS)::value;
-      if constexpr (ks + 1 < NKS)
-        load_frags(as, bs, std::integral_constant<int, ks + 1>{}, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
+  // ---- pipelined mainloop --------------------------------------------------
+  // The K dimension is a stream of MFMA K-steps (NKS per tile).  The fragments
+  // of step s+1 are read from LDS while the MFMAs of step s issue, across tile
+  // boundaries too, so a wave never waits on LDS latency at the start of a
+  // tile.  The LDS ring holds STAGES tiles.  Barrier B(kt) sits before the last
+  // K-step of tile kt: by then every wave has read all fragments of tile kt
+  // (they were read during the previous step), so B(kt) both publishes tile
+  // kt+1 (each wave first waits for its own loads of it) and retires stage
+  // kt % STAGES, which is refilled at once with tile kt+STAGES.  After the
+  // barrier the wave goes straight to MFMAs on fragments already in registers.
+  //
+  // Past the last tile the fetch index is clamped to nk-1 (a re-read of a
+  // cached tile into a stage nobody reads again), so every step issues exactly
+  // LOADS loads and the vmcnt threshold is a constant.
+  constexpr int DS_PER_KS = G::TM * (ESZ == 2 ? 1 : 2) + G::TN * (ESZ == 2 ? 2 : 4);
+  constexpr int MFMA_PER_KS = G::TM * G::TN;
+  static_assert(STAGES == 2 || (G::A_EVEN && G::B_EVEN), "vmcnt accounting needs every lane loading");
+  static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
+  static_assert((STAGES * NKS) % 2 == 0, "fragment double buffer parity must repeat every STAGES tiles");
+  constexpr bool EXACT_VMCNT = G::A_EVEN && G::B_EVEN;
+
+  Frag fa[2][G::TM], fb[2][G::TN];
+  auto mfma_step = [&](const Frag* af, const Frag* bf) ICPP_INLINE {
 #pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm)
+    for (int tm = 0; tm < G::TM; ++tm)
 #pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn) acc[tm][tn] = Op::run(bf[ks & 1][tn], af[ks & 1][tm], acc[tm][tn]);
-    });
-    // Issue order for the scheduler: the reads of step 0, then for every later
-    // step its reads spread evenly between the MFMAs of the step before (left
-    // alone, the backend re-reads fragments just before use and waits on each).
-    constexpr int DS_PER_KS = G::TM * (ESZ == 2 ? 1 : 2) + G::TN * (ESZ == 2 ? 2 : 4);
-    constexpr int MFMA_PER_KS = G::TM * G::TN;
-    __builtin_amdgcn_sched_group_barrier(0x100, DS_PER_KS, 0);
-    static_for<NKS>([&](auto KS) ICPP_INLINE {
-      constexpr int ks = decltype(KS)::value;
-      if constexpr (ks + 1 < NKS) {
-        static_for<MFMA_PER_KS>([&](auto I) ICPP_INLINE {
-          constexpr int i = decltype(I)::value;
-          constexpr int ds = (i + 1) * DS_PER_KS / MFMA_PER_KS - i * DS_PER_KS / MFMA_PER_KS;
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);
-        });
-      } else {
-        __builtin_amdgcn_sched_group_barrier(0x008, MFMA_PER_KS, 0);
-      }
+      for (int tn = 0; tn < G::TN; ++tn) acc[tm][tn] = Op::run(bf[tn], af[tm], acc[tm][tn]);
+  };
+  // Issue order for the scheduler within one K-step: its MFMAs one by one, with
+  // the next step's fragment reads (left alone, the backend re-reads fragments
+  // just before use and waits on each) and NL tile loads (issued as one burst
+  // they stall the wave on the vector-memory queue -- the CU's texture path
+  // takes ~16 cycles per 1 KiB load -- ahead of its MFMAs) spread between the
+  // first SPAN of them, so the reads have landed by the next barrier.
+  auto schedule = [&](auto NL) ICPP_INLINE {
+    constexpr int nl_total = decltype(NL)::value;
+    constexpr int SPAN = (MFMA_PER_KS * 3) / 4 > 0 ? (MFMA_PER_KS * 3) / 4 : 1;
+    static_for<MFMA_PER_KS>([&](auto I) ICPP_INLINE {
+      constexpr int i = decltype(I)::value;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      // items x with floor(x * SPAN / total) == i follow MFMA i
+      constexpr int ds = (i < SPAN) ? ((i + 1) * DS_PER_KS + SPAN - 1) / SPAN - (i * DS_PER_KS + SPAN - 1) / SPAN : 0;
+      if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);
+      constexpr int nl = (i < SPAN) ? ((i + 1) * nl_total + SPAN - 1) / SPAN - (i * nl_total + SPAN - 1) / SPAN : 0;
+      if constexpr (nl > 0) __builtin_amdgcn_sched_group_barrier(0x020, nl, 0);
     });
   };
 
-  // ---- pipelined mainloop: STAGES-deep LDS ring, one barrier per K tile ----
-  // Tile kt+STAGES-1 is fetched into the stage that tile kt-1 used while tile kt
-  // is multiplied; the barrier at the top of iteration kt both publishes tile
-  // kt (after this wave's own loads for it completed) and retires stage kt-1.
-  constexpr int LOADS = G::SA + G::SB;  // loads per thread per tile (all threads: A_EVEN && B_EVEN for STAGES > 2)
-  static_for<STAGES - 1>([&](auto S) ICPP_INLINE {
-    if (decltype(S)::value < nk) issue_tile(decltype(S)::value, S);
-  });
+  static_for<STAGES>([&](auto S) ICPP_INLINE { issue_tile(min((int)decltype(S)::value, nk - 1), S); });
+  if constexpr (EXACT_VMCNT) wait_vmcnt<(STAGES - 1) * LOADS>();
+  else wait_vmcnt<0>();
+  lds_barrier();  // tile 0 published
+  load_frags(stage_base(std::integral_constant<int, 0>{}), stage_base(std::integral_constant<int, 0>{}) + G::A_BYTES,
+             std::integral_constant<int, 0>{}, fa[0], fb[0]);
   for (int kt0 = 0; kt0 < nk; kt0 += STAGES) {
-    // the stage index of each step is a compile-time constant: kt0 % STAGES == 0
+    // the stage index of each tile is a compile-time constant: kt0 % STAGES == 0
     static_for<STAGES>([&](auto J) ICPP_INLINE {
       constexpr int j = decltype(J)::value;
       const int kt = kt0 + j;
       if (kt < nk) {
-        if constexpr (STAGES > 2) {
-          if (nk - 1 - kt >= STAGES - 2) wait_vmcnt<(STAGES - 2) * LOADS>();
-          else wait_vmcnt<0>();
-        } else {
-          wait_vmcnt<0>();
-        }
-        __syncthreads();
-        if (kt + STAGES - 1 < nk) issue_tile(kt + STAGES - 1, std::integral_constant<int, (j + STAGES - 1) % STAGES>{});
-        compute(J);
+        const char ICPP_LDS* as = stage_base(J);
+        static_for<NKS>([&](auto KS) ICPP_INLINE {
+          constexpr int ks = decltype(KS)::value;
+          constexpr int s = j * NKS + ks;  // position in the fragment double buffer
+          if constexpr (ks + 1 < NKS) {
+            load_frags(as, as + G::A_BYTES, std::integral_constant<int, ks + 1>{}, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            mfma_step(fa[s & 1], fb[s & 1]);
+            schedule(std::integral_constant<int, 0>{});
+          } else {
+            wait_vmcnt<(STAGES - 2) * LOADS>();  // this wave's loads of tile kt+1 landed
+            lds_barrier();                        // B(kt): tile kt+1 published, stage j retired
+            issue_tile(min(kt + STAGES, nk - 1), J);
+            constexpr int jn = (j + 1) % STAGES;
+            const char ICPP_LDS* an = stage_base(std::integral_constant<int, jn>{});
+            load_frags(an, an + G::A_BYTES, std::integral_constant<int, 0>{}, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            mfma_step(fa[s & 1], fb[s & 1]);
+            schedule(std::integral_constant<int, LOADS>{});
+          }
+        });
       }
     });
   }
+  wait_vmcnt<0>();  // no LDS-DMA write may land after this point (epilogue staging, next workgroup)
 
   // ---- epilogue ----
   // lane owns output row (lane % MF) of each MFMA tile and groups of 4 consecutive columns
@@ -637,7 +686,9 @@ gemm_kernel(KArgs p) {
     constexpr int PER_STAGE = G::STAGE_BYTES / REGION;  // wave regions per stage array
     static_assert(PER_STAGE * STAGES >= WM * WN, "epilogue staging must fit the LDS stages");
     static_assert((G::WTN * OSZ) % 16 == 0, "wave tile rows must be whole 16-byte chunks");
-    OutT* C = (OutT*)p.C;
+    // store descriptor over this tile's rows (launchers keep BM * ldc * OSZ < 2 GiB)
+    const uint64_t rows = (uint64_t)(p.M > row0 ? min(p.M - row0, BM) : 0);
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc((OutT*)p.C + (size_t)row0 * p.ldc, (uint32_t)(rows * p.ldc * OSZ));
     const int w_arr = wave / PER_STAGE;
     char ICPP_LDS* arr = (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
                        : (w_arr == 2) ? (char ICPP_LDS*)lds2 : (char ICPP_LDS*)lds3;
@@ -662,9 +713,10 @@ gemm_kernel(KArgs p) {
         if ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O) {
           const int rr = q / CPR_O, cc = q % CPR_O;
           const i32x4 v = *(const i32x4 ICPP_LDS*)(region + rr * ROWB_O + cc * 16);
-          const int m = row0 + wm * G::WTM + tm * MF + rr;
+          const int r = wm * G::WTM + tm * MF + rr;  // row within the tile: rows >= M lie past the range
           const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
-          if (m < p.M && n < p.N) *(i32x4*)(C + (size_t)m * p.ldc + n) = v;
+          const uint32_t off = (uint32_t)(r * p.ldc + n) * OSZ;
+          buf_store16(rc, n < p.N ? off : ICPP_OOB_OFFSET, v);
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -697,11 +749,13 @@ gemm_kernel(KArgs p) {
           const int n = out_col(tn, g);
           bv[tn][g] = (bias != nullptr && n < p.N) ? Vec4Store<BiasT>::ld(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
-      store_staged([&](int tm, int tn, int g) {
-        f32x4 v = get4(tm, tn, g);
+      dispatch_act(p.act, [&](auto ACT) ICPP_INLINE {
+        store_staged([&](int tm, int tn, int g) ICPP_INLINE {
+          f32x4 v = get4(tm, tn, g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e] * p.alpha + bv[tn][g][e], p.act);
-        return v;
+          for (int e = 0; e < 4; ++e) v[e] = act_fn<decltype(ACT)::value>(v[e] * p.alpha + bv[tn][g][e]);
+          return v;
+        });
       });
     }
   } else {
@@ -865,8 +919,10 @@ splitk_reduce_kernel(const float* __restrict__ ws, void* C, const void* bias, in
     for (int z = 0; z < splits; ++z) s += Vec4Store<float>::ld(ws + ((size_t)z * M + m) * N + n);
     f32x4 bv = {0.f, 0.f, 0.f, 0.f};
     if (bias != nullptr) bv = Vec4Store<BiasT>::ld((const BiasT*)bias + n);
+    dispatch_act(act, [&](auto ACT) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s[e] = apply_act(s[e] * alpha + bv[e], act);
+      for (int e = 0; e < 4; ++e) s[e] = act_fn<decltype(ACT)::value>(s[e] * alpha + bv[e]);
+    });
     Vec4Store<OutT>::st((OutT*)C + (size_t)m * ldc + n, s);
   }
 }
