@@ -228,7 +228,7 @@ def main():
             return 2
         cfg, tuned = raw_from_inst(match[0]), None
     else:
-        res = tune(desc, top_k=4, warmup=2, reps=5, M=M, N=N, K=K)
+        res = tune(desc, top_k=4, warmup=3, reps=10, M=M, N=N, K=K)
         cfg, tuned = res.best_config, res
     kern = GBA.build_kernel(M, N, K, config=cfg, act="gelu_tanh", dtype="bf16")
     d = I.config2(M, N, K, device="cuda")
