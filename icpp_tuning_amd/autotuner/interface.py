@@ -145,12 +145,17 @@ class TuneResult:
         return dict(self.__dict__)
 
 
-def benchmark_ms(fn, warmup: int = 3, reps: int = 10, batches: int = 3) -> float:
-    """Per-launch device time in ms: HIP events on the current stream around
-    ``reps`` back-to-back launches (the way the reference times conv2d,
-    conv2d.py:171-183), median over ``batches``.  A single launch between two
-    events carries ~10-20 us of event / dispatch overhead on ROCm, which would
-    swamp kernels of a few microseconds.
+def benchmark_ms(fn, warmup: int = 3, reps: int = 10, batches: int = 3, graph: bool = True) -> float:
+    """Per-launch device time in ms: HIP events around ``reps`` back-to-back
+    launches (the way the reference times conv2d, conv2d.py:171-183), median
+    over ``batches``.
+
+    With ``graph`` the ``reps`` launches are captured once into a HIP graph and
+    the graph is replayed between the events, so the figure is the device time
+    of the kernels themselves: issuing a launch from Python (argument checks +
+    the ctypes call) costs ~10 us, more than a small kernel runs, and an eager
+    loop would time the host instead.  Capture failures fall back to the eager
+    loop.
 
     ``fn`` is a callable, or a list of callables used round-robin (distinct
     input copies, so that a working set larger than the caches stays cold)."""
@@ -160,12 +165,28 @@ def benchmark_ms(fn, warmup: int = 3, reps: int = 10, batches: int = 3) -> float
     for i in range(max(warmup, len(fns))):
         fns[i % len(fns)]()
     torch.cuda.synchronize()
+
+    def launch_all():
+        for i in range(reps):
+            fns[i % len(fns)]()
+
+    run = launch_all
+    if graph:
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                launch_all()
+            g.replay()
+            torch.cuda.synchronize()
+            run = g.replay
+        except Exception:  # noqa: BLE001 - capture unsupported here: time the eager loop
+            torch.cuda.synchronize()
+            run = launch_all
     times = []
     for _ in range(batches):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        for i in range(reps):
-            fns[i % len(fns)]()
+        run()
         e.record()
         e.synchronize()
         times.append(s.elapsed_time(e) / reps)

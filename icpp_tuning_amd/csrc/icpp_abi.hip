@@ -157,10 +157,11 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
   a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
   a.act = act; a.alpha = scale_a * scale_b;
   a.k_split = K / split_k;
+  a.splits = split_k;
   a.tiles_m = ceil_div(M, t.block_m);
   a.tiles_n = ceil_div(N, t.block_n);
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(a.tiles_m * a.tiles_n, split_k);
+  const dim3 grid(a.tiles_m * a.tiles_n * split_k);  // one workgroup per (tile, K split) item
   if (split_k > 1) {
     const size_t need = (size_t)split_k * M * N * sizeof(float);
     if (!workspace || ws_bytes < need || !aligned16(workspace))
@@ -195,10 +196,11 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
   a.A = A; a.B = B; a.bias = bias; a.C = Y; a.gamma = gamma; a.beta = beta;
   a.M = M; a.N = N; a.K = K; a.lda = K; a.ldb = N; a.ldc = N; a.eps = eps;
   a.k_split = K;
+  a.splits = 1;
   a.tiles_m = ceil_div(M, t.block_m);
   a.tiles_n = ceil_div(N, t.block_n);
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(a.tiles_m * a.tiles_n, 1);
+  const dim3 grid(a.tiles_m * a.tiles_n);
   if (family == ICPP_FAMILY_GEMM_LN_ROW) {
     if (a.tiles_n != 1) return fail(ICPP_E_SHAPE, "row LayerNorm instance %s needs N <= block_n (N=%d)", t.name, N);
     return check_launch(in->launch(a, grid, s), t.name);
@@ -243,24 +245,27 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   a.A = X; a.B = Wt; a.C = Y;
   a.M = (int)Mg; a.N = F; a.K = (int)Kg; a.lda = 0; a.ldb = F; a.ldc = F;
   a.k_split = (int)Kg / split_k;
+  a.splits = split_k;
   a.tiles_m = ceil_div(a.M, t.block_m);
   a.tiles_n = ceil_div(F, t.block_n);
-  a.cH = H; a.cW = W; a.cC = C; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH; a.cOW = OW;
+  a.cH = H; a.cW = W; a.cC = C; a.cKH = KH; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH;
+  a.cOW = OW;
   a.a_bytes_total = (uint32_t)xbytes;
-  a.tap_uniform = (C % t.block_k == 0) ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(a.tiles_m * a.tiles_n, split_k);
+  // every K tile inside one filter tap (and the tap set fits the 64-bit mask): per-tile-tap gather
+  const LaunchFn launch = (C % t.block_k == 0 && KH * KW <= 64) ? in->launch : in->launch_gather;
+  const dim3 grid(a.tiles_m * a.tiles_n * split_k);  // one workgroup per (tile, K split) item
   if (split_k > 1) {
     const size_t need = (size_t)split_k * a.M * F * sizeof(float);
     if (!workspace || ws_bytes < need || !aligned16(workspace))
       return fail(ICPP_E_WORKSPACE, "icpp_conv2d_nhwc: split_k=%d needs %zu workspace bytes (got %zu)", split_k, need, ws_bytes);
     a.partial = 1;
     a.ws = (float*)workspace;
-    int rc = check_launch(in->launch(a, grid, s), t.name);
+    int rc = check_launch(launch(a, grid, s), t.name);
     if (rc) return rc;
     return check_launch(launch_splitk_reduce(DT_F16, a.ws, Y, nullptr, a.M, F, F, split_k, 1.f, ICPP_ACT_NONE, s), "splitk_reduce");
   }
-  return check_launch(in->launch(a, grid, s), t.name);
+  return check_launch(launch(a, grid, s), t.name);
 }
 
 }  // extern "C"

@@ -39,7 +39,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 enum DType { DT_F16 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_F32 = 3 };
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3 };
 enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
-enum ALoad { A_DENSE = 0, A_IM2COL = 1 };
+// A operand loaders: dense rows, the NHWC implicit-GEMM gather for any C
+// (per 16-byte chunk), and the gather for C % BK == 0, where every K tile is one
+// filter tap so the tap decomposition is per tile rather than per chunk.
+enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -69,14 +72,14 @@ struct KArgs {
   int act;
   float alpha;        // scale_a * scale_b (fp8), 1 otherwise
   float eps;
-  int k_split;        // K elements per split slice (multiple of BK)
+  int k_split;        // K elements per split slice (multiple of BK); K == splits * k_split
+  int splits;         // K slices (split-K); items = tiles_m * tiles_n * splits
   int tiles_m, tiles_n;
   int stat_cols;      // LN stats columns per row
-  int partial;        // 1: store fp32 partials to ws[blockIdx.y]
-  // implicit-GEMM conv geometry (A_IM2COL); GEMM M = Nb*OH*OW, K = KH*KW*C
-  int cH, cW, cC, cKW, cS, cP, cD, cOH, cOW;
+  int partial;        // 1: store fp32 partials to ws[split]
+  // implicit-GEMM conv geometry (A_IM2COL*); GEMM M = Nb*OH*OW, K = KH*KW*C
+  int cH, cW, cC, cKH, cKW, cS, cP, cD, cOH, cOW;
   uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
-  int tap_uniform;         // C % BK == 0: every K tile lies inside one filter tap
 };
 
 template <int DT> struct DTraits;
@@ -292,8 +295,7 @@ struct Tile {
   static_assert(LDS_BYTES <= 160 * 1024, "LDS overflow");
 
   static_assert(A_CHUNKS % 64 == 0 && B_CHUNKS % 64 == 0, "tile loads must cover whole waves");
-  static_assert(STAGES == 2 || (A_EVEN && B_EVEN), "deeper LDS rings need every thread to issue every load");
-  static_assert((SA + SB) * (STAGES > 2 ? STAGES - 2 : 0) < 64, "vmcnt range");
+  static_assert((SA + SB) * (STAGES - 1) < 64, "vmcnt range");
 
   // A: row r, logical 16 B chunk c -> byte offset in the A region
   static __device__ __forceinline__ int a_swz(int r) { return (r / RPB_A) % SWZ_A; }
@@ -364,23 +366,27 @@ gemm_kernel(KArgs p) {
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  // ---- tile index: XCD-contiguous ranges of the grid, then grouped-M order ----
-  int t = blockIdx.x;
+  // ---- work item ----
+  // An item is one output tile of one K split; a launch has one workgroup per
+  // item.  The grid is remapped so each XCD takes a contiguous range of slots;
+  // items are ordered split-major, then in groups of 8 tile rows (grouped-M)
+  // so neighbouring slots share B panels in L2.
+  struct Item { int row0, col0, kz; };
+  const int tiles = p.tiles_m * p.tiles_n;
   const int nb = gridDim.x;
-  if ((nb & 7) == 0) t = (t & 7) * (nb >> 3) + (t >> 3);
-  const int GROUP = 8;
-  const int group_size = GROUP * p.tiles_n;
-  const int group = t / group_size;
-  const int first_m = group * GROUP;
-  const int gm = min(p.tiles_m - first_m, GROUP);
-  const int tile_m = first_m + (t % group_size) % gm;
-  const int tile_n = (t % group_size) / gm;
-  const int row0 = tile_m * BM, col0 = tile_n * BN;
-
-  const int kz = blockIdx.y;
-  const int k_begin = kz * p.k_split;
-  const int k_len = min(p.k_split, p.K - k_begin);
-  const int nk = k_len / BK;
+  int slot = blockIdx.x;
+  if ((nb & 7) == 0) slot = (slot & 7) * (nb >> 3) + (slot >> 3);
+  auto item_of = [&](int it) ICPP_INLINE {
+    const int kz = it / tiles;
+    const int t = it - kz * tiles;
+    constexpr int GROUP = 8;
+    const int group_size = GROUP * p.tiles_n;
+    const int first_m = (t / group_size) * GROUP;
+    const int gm = min(p.tiles_m - first_m, GROUP);
+    return Item{(first_m + (t % group_size) % gm) * BM, ((t % group_size) / gm) * BN, kz};
+  };
+  const int nk = p.k_split / BK;  // K tiles of the item
+  const Item first = item_of(slot);
 
   // ---- global -> LDS: buffer_load_dwordx4 ... lds (16 B per lane, range-checked:
   // out-of-range lanes deliver zeros).  Load i of wave w writes LDS chunks
@@ -393,63 +399,105 @@ gemm_kernel(KArgs p) {
   const char* Ab = (const char*)p.A;
   const char* Bb = (const char*)p.B;
   __amdgpu_buffer_rsrc_t ra, rb;
-  if constexpr (ALOAD == A_DENSE) {
-    const uint64_t rem = (uint64_t)(p.M > row0 ? p.M - row0 : 0) * (uint64_t)p.lda * ESZ;
-    ra = make_rsrc(Ab + (size_t)row0 * p.lda * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
-  } else {
-    ra = make_rsrc(Ab, (uint32_t)p.a_bytes_total);
-  }
-  {
-    const uint64_t rem = ((uint64_t)(p.K - 1) * p.ldb + (uint64_t)(p.N - col0)) * ESZ;
-    rb = make_rsrc(Bb + (size_t)col0 * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
-  }
   constexpr bool A_UNIFORM = (ALOAD == A_DENSE) && (G::THREADS % G::CPR_A == 0) &&
                              ((G::THREADS / G::CPR_A) % (G::RPB_A * G::SWZ_A) == 0);
   constexpr bool B_UNIFORM = (G::THREADS % G::CPR_B == 0) && ((G::THREADS / G::CPR_B) % G::B_SWZ_PERIOD == 0);
   constexpr int NA = A_UNIFORM ? 1 : G::SA;
   constexpr int NB = B_UNIFORM ? 1 : G::SB;
-  uint32_t a_goff[NA];
-  int a_lc[ALOAD == A_IM2COL ? G::SA : 1];
-  int a_img[ALOAD == A_IM2COL ? G::SA : 1], a_ih0[ALOAD == A_IM2COL ? G::SA : 1], a_iw0[ALOAD == A_IM2COL ? G::SA : 1];
-  int a_pix[ALOAD == A_IM2COL ? G::SA : 1];  // NHWC pixel index of the (kh, kw) = (0, 0) tap
+  constexpr bool GATHER = ALOAD == A_IM2COL, TAPS = ALOAD == A_IM2COL_TAP;
+  uint32_t a_goff[NA];  // per-lane A byte offset within the item's rows, K offset excluded
+  // general gather: chunk column, image (-1 past M) and the (0, 0)-tap input coordinates
+  int a_lc[GATHER ? G::SA : 1], a_img[GATHER ? G::SA : 1], a_ih0[GATHER ? G::SA : 1], a_iw0[GATHER ? G::SA : 1];
+  // per-tile-tap gather: byte offset of the chunk at tap (0, 0) (may be negative
+  // at the padding border) and the set of taps that land inside the image
+  int a_tbase[TAPS ? G::SA : 1];
+  uint64_t a_tmask[TAPS ? G::SA : 1];
+  // Point the loaders at item it: buffer descriptors at its rows / columns and,
+  // for the conv gathers, each lane's input coordinates for its output row.
+  auto setup_issue = [&](const Item& it) ICPP_INLINE {
+    const int row0 = it.row0, col0 = it.col0;
+    if constexpr (ALOAD == A_DENSE) {
+      const uint64_t rem = (uint64_t)(p.M > row0 ? p.M - row0 : 0) * (uint64_t)p.lda * ESZ;
+      ra = make_rsrc(Ab + (size_t)row0 * p.lda * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
+    } else {
+      ra = make_rsrc(Ab, (uint32_t)p.a_bytes_total);
+    }
+    {
+      const uint64_t rem = ((uint64_t)(p.K - 1) * p.ldb + (uint64_t)(p.N - col0)) * ESZ;
+      rb = make_rsrc(Bb + (size_t)col0 * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
+    }
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int q = tid + i * G::THREADS;
     const int r = q / G::CPR_A;
     const int c = (q % G::CPR_A) ^ G::a_swz(r);
     if constexpr (ALOAD == A_DENSE) {
-      a_goff[i] = (uint32_t)(r * p.lda * ESZ + (k_begin + c * G::CH) * ESZ);
+      a_goff[i] = (uint32_t)(r * p.lda * ESZ + c * G::CH * ESZ);
     } else {
-      a_lc[i] = c;
       const int m = row0 + r;
       const int ohw = p.cOH * p.cOW;
       const int img = m / ohw;
       const int rem = m - img * ohw;
       const int oh = rem / p.cOW, ow = rem - (rem / p.cOW) * p.cOW;
-      a_img[i] = (m < p.M) ? img : -1;
-      a_ih0[i] = oh * p.cS - p.cP;
-      a_iw0[i] = ow * p.cS - p.cP;
-      a_pix[i] = (img * p.cH + a_ih0[i]) * p.cW + a_iw0[i];
+      const int ih0 = oh * p.cS - p.cP, iw0 = ow * p.cS - p.cP;
+      if constexpr (GATHER) {
+        a_lc[i] = c;
+        a_img[i] = (m < p.M) ? img : -1;
+        a_ih0[i] = ih0;
+        a_iw0[i] = iw0;
+      } else {
+        a_tbase[i] = (((img * p.cH + ih0) * p.cW + iw0) * p.cC + c * G::CH) * ESZ;
+        uint64_t mk = 0;
+        if (m < p.M) {
+          for (int tap = 0, kh = 0, kw = 0; tap < p.cKH * p.cKW; ++tap) {
+            const int ih = ih0 + kh * p.cD, iw = iw0 + kw * p.cD;
+            if ((unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW) mk |= 1ull << tap;
+            if (++kw == p.cKW) { kw = 0; ++kh; }
+          }
+        }
+        a_tmask[i] = mk;
+      }
       a_goff[i] = 0;
     }
   }
-  uint32_t b_goff[NB];
+  };
+  setup_issue(first);
+  uint32_t b_goff[NB];  // per-lane B byte offset within the item's columns, K offset excluded
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     const int q = tid + i * G::THREADS;
     const int k = q / G::CPR_B;
     const int c = (q % G::CPR_B) ^ G::b_swz(k);
-    b_goff[i] = (uint32_t)((k_begin + k) * p.ldb * ESZ + c * 16);
+    b_goff[i] = (uint32_t)(k * p.ldb * ESZ + c * 16);
   }
   const uint32_t a_row_step = (uint32_t)((G::THREADS / G::CPR_A) * p.lda * ESZ);  // bytes per load (A_UNIFORM)
   const uint32_t b_row_step = (uint32_t)((G::THREADS / G::CPR_B) * p.ldb * ESZ);  // bytes per load (B_UNIFORM)
   // byte offset of this wave's lane 0 within one load (wave-uniform -> SGPR)
   const int wave_slot = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 16;
 
-  // One 16-byte-per-lane load of tile kt into stage S: loads 0 .. SA-1 move A
-  // chunks, SA .. SA+SB-1 move B chunks.  Issued one at a time so the mainloop
-  // can spread them between the MFMAs of the tile being multiplied.
-  auto issue_load = [&](int kt, auto S, auto L) ICPP_INLINE {
+  // Per-tile part of the A address shared by all loads of the tile starting at
+  // K element kk.  For the per-tile-tap gather (C % BK == 0) that tile is filter
+  // tap `tap` and channels c0 .. c0+BK-1 of it: scalar work once per tile, after
+  // which a lane's offset is its tap-(0,0) base plus a tile constant, or past
+  // the buffer (zeros) when the tap falls in the padding.
+  struct TileCtx { int tap; int toff; };
+  auto tile_ctx = [&](int kk) ICPP_INLINE {
+    TileCtx t{0, 0};
+    if constexpr (TAPS) {
+      const int kg = kk / BK;  // global K-tile index
+      const int tiles_per_tap = p.cC / BK;
+      const int tap = kg / tiles_per_tap;
+      const int c0 = (kg - tap * tiles_per_tap) * BK;
+      const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
+      t.tap = tap;
+      t.toff = ((kh * p.cD * p.cW + kw * p.cD) * p.cC + c0) * ESZ;
+    }
+    return t;
+  };
+  // One 16-byte-per-lane load of the tile at K element kk into stage S: loads
+  // 0 .. SA-1 move A chunks, SA .. SA+SB-1 move B chunks.  Issued one at a time
+  // so the mainloop can spread them between the MFMAs of the tile being multiplied.
+  auto issue_load = [&](int kk, auto S, auto L, const TileCtx& tc) ICPP_INLINE {
     constexpr int l = decltype(L)::value;
     char ICPP_LDS* as = stage_base(S);
     char ICPP_LDS* bs = as + G::A_BYTES;
@@ -458,27 +506,16 @@ gemm_kernel(KArgs p) {
       if (!(G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS)) return;
       if constexpr (ALOAD == A_DENSE) {
         if constexpr (A_UNIFORM)
-          dma16(ra, a_goff[0], (uint32_t)(kt * BK * ESZ) + i * a_row_step, as + i * G::THREADS * 16 + wave_slot);
+          dma16(ra, a_goff[0], (uint32_t)(kk * ESZ) + i * a_row_step, as + i * G::THREADS * 16 + wave_slot);
         else
-          dma16(ra, a_goff[i], (uint32_t)(kt * BK * ESZ), as + i * G::THREADS * 16 + wave_slot);
-      } else if (p.tap_uniform) {
-        // The whole K tile is one filter tap (kh, kw) and channels c0 .. c0+BK-1:
-        // the tap decomposition is wave-uniform scalar work, each lane adds a
-        // constant pixel delta to its precomputed base and checks the padding.
-        const int kbase = k_begin + kt * BK;
-        const int tap = __builtin_amdgcn_readfirstlane(kbase / p.cC);
-        const int c0 = kbase - tap * p.cC;
-        const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
-        const int dh = kh * p.cD, dw = kw * p.cD;
-        const int pix_delta = dh * p.cW + dw;
-        const int ih = a_ih0[i] + dh, iw = a_iw0[i] + dw;
-        const bool ok = a_img[i] >= 0 && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW;
-        const uint32_t off = ok ? (uint32_t)(((a_pix[i] + pix_delta) * p.cC + c0 + a_lc[i] * G::CH) * ESZ)
-                                : (uint32_t)p.a_bytes_total;
+          dma16(ra, a_goff[i], (uint32_t)(kk * ESZ), as + i * G::THREADS * 16 + wave_slot);
+      } else if constexpr (TAPS) {
+        const bool ok = (a_tmask[i] >> tc.tap) & 1u;
+        const uint32_t off = ok ? (uint32_t)(a_tbase[i] + tc.toff) : p.a_bytes_total;
         dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
       } else {
         // K index of this chunk -> (kh, kw, c); one filter tap per chunk since C % 8 == 0
-        const int k = k_begin + kt * BK + a_lc[i] * G::CH;
+        const int k = kk + a_lc[i] * G::CH;
         const int tap = k / p.cC;
         const int ci = k - tap * p.cC;
         const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
@@ -492,14 +529,15 @@ gemm_kernel(KArgs p) {
       constexpr int i = l - G::SA;
       if (!(G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS)) return;
       if constexpr (B_UNIFORM)
-        dma16(rb, b_goff[0], (uint32_t)(kt * BK * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
+        dma16(rb, b_goff[0], (uint32_t)(kk * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
       else
-        dma16(rb, b_goff[i], (uint32_t)(kt * BK * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
+        dma16(rb, b_goff[i], (uint32_t)(kk * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
     }
   };
   constexpr int LOADS = G::SA + G::SB;  // loads per thread per tile
-  auto issue_tile = [&](int kt, auto S) ICPP_INLINE {
-    static_for<LOADS>([&](auto L) ICPP_INLINE { issue_load(kt, S, L); });
+  auto issue_tile = [&](int kk, auto S) ICPP_INLINE {
+    const TileCtx tc = tile_ctx(kk);
+    static_for<LOADS>([&](auto L) ICPP_INLINE { issue_load(kk, S, L, tc); });
   };
 
   Acc acc[G::TM][G::TN];
@@ -594,10 +632,25 @@ gemm_kernel(KArgs p) {
   // LOADS loads and the vmcnt threshold is a constant.
   constexpr int DS_PER_KS = G::TM * (ESZ == 2 ? 1 : 2) + G::TN * (ESZ == 2 ? 2 : 4);
   constexpr int MFMA_PER_KS = G::TM * G::TN;
-  static_assert(STAGES == 2 || (G::A_EVEN && G::B_EVEN), "vmcnt accounting needs every lane loading");
-  static_assert((STAGES - 1) * LOADS < 64, "vmcnt range");
   static_assert((STAGES * NKS) % 2 == 0, "fragment double buffer parity must repeat every STAGES tiles");
-  constexpr bool EXACT_VMCNT = G::A_EVEN && G::B_EVEN;
+  // Loads this wave issues per tile.  Tile loads cover whole waves (chunk
+  // counts are multiples of 64), so in the last, partial round of A or B loads
+  // a wave either loads or skips as a whole: per wave the count is LOADS,
+  // LOADS-1 or LOADS-2, and vmcnt thresholds follow it.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int my_loads = (G::A_CHUNKS > 64 * wv ? (G::A_CHUNKS - 64 * wv + G::THREADS - 1) / G::THREADS : 0) +
+                       (G::B_CHUNKS > 64 * wv ? (G::B_CHUNKS - 64 * wv + G::THREADS - 1) / G::THREADS : 0);
+  // s_waitcnt vmcnt(TILES * my_loads): at most TILES tiles of this wave's loads still in flight
+  auto wait_tiles = [&](auto TILES) ICPP_INLINE {
+    constexpr int nt = decltype(TILES)::value;
+    if constexpr (nt == 0 || (G::A_EVEN && G::B_EVEN)) {
+      wait_vmcnt<nt * LOADS>();
+    } else {
+      if (my_loads == LOADS) wait_vmcnt<nt * LOADS>();
+      else if (my_loads == LOADS - 1) wait_vmcnt<nt * (LOADS - 1)>();
+      else wait_vmcnt<nt * (LOADS >= 2 ? LOADS - 2 : 0)>();
+    }
+  };
 
   Frag fa[2][G::TM], fb[2][G::TN];
   auto mfma_step = [&](const Frag* af, const Frag* bf) ICPP_INLINE {
@@ -626,14 +679,264 @@ gemm_kernel(KArgs p) {
     });
   };
 
-  static_for<STAGES>([&](auto S) ICPP_INLINE { issue_tile(min((int)decltype(S)::value, nk - 1), S); });
-  if constexpr (EXACT_VMCNT) wait_vmcnt<(STAGES - 1) * LOADS>();
-  else wait_vmcnt<0>();
+  // ---- epilogue of one item ----
+  auto epilogue = [&](const Item& it) ICPP_INLINE {
+    const int row0 = it.row0, col0 = it.col0, kz = it.kz;
+    // lane owns output row (lane % MF) of each MFMA tile and groups of 4 consecutive columns
+    constexpr int NG = Op::ACC / 4;  // column groups per MFMA tile
+    auto out_row = [&](int tm) ICPP_INLINE { return row0 + wm * G::WTM + tm * MF + (lane % MF); };
+    auto out_col = [&](int tn, int g) ICPP_INLINE {
+      return col0 + wn * G::WTN + tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
+    };
+    auto get4 = [&](int tm, int tn, int g) ICPP_INLINE {
+      return f32x4{acc[tm][tn][4 * g + 0], acc[tm][tn][4 * g + 1], acc[tm][tn][4 * g + 2], acc[tm][tn][4 * g + 3]};
+    };
+
+    // Output through LDS: for each MFMA row band (tm) a wave writes its values
+    // (converted to OutT) into a private padded LDS region, then re-reads them as
+    // 16-byte row chunks, so global stores cover whole contiguous row segments
+    // instead of 8-byte pieces of 16 different rows.
+    auto store_staged = [&](auto&& value4) ICPP_INLINE {
+      constexpr int OSZ = (int)sizeof(OutT);
+      constexpr int ROWB_O = G::WTN * OSZ + 16;           // +16 B rotates rows across banks
+      constexpr int REGION = MF * ROWB_O;
+      constexpr int CPR_O = G::WTN * OSZ / 16;             // 16-byte chunks per output row
+      constexpr int CHUNK_ELEMS = 16 / OSZ;
+      constexpr int PER_STAGE = G::STAGE_BYTES / REGION;  // wave regions per stage array
+      static_assert(PER_STAGE * STAGES >= WM * WN, "epilogue staging must fit the LDS stages");
+      static_assert((G::WTN * OSZ) % 16 == 0, "wave tile rows must be whole 16-byte chunks");
+      // store descriptor over this tile's rows (launchers keep BM * ldc * OSZ < 2 GiB)
+      const uint64_t rows = (uint64_t)(p.M > row0 ? min(p.M - row0, BM) : 0);
+      const __amdgpu_buffer_rsrc_t rc = make_rsrc((OutT*)p.C + (size_t)row0 * p.ldc, (uint32_t)(rows * p.ldc * OSZ));
+      const int w_arr = wave / PER_STAGE;
+      char ICPP_LDS* arr = (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
+                         : (w_arr == 2) ? (char ICPP_LDS*)lds2 : (char ICPP_LDS*)lds3;
+      char ICPP_LDS* region = arr + (wave % PER_STAGE) * REGION;
+      __syncthreads();  // every wave is done reading the pipeline stages
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const f32x4 v = value4(tm, tn, g);
+            const int lcol = tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
+            Vec4Store<OutT>::st_lds(region + (lane % MF) * ROWB_O + lcol * OSZ, v);
+          }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q0 = 0; q0 < MF * CPR_O; q0 += 64) {
+          const int q = q0 + lane;
+          if ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O) {
+            const int rr = q / CPR_O, cc = q % CPR_O;
+            const i32x4 v = *(const i32x4 ICPP_LDS*)(region + rr * ROWB_O + cc * 16);
+            const int r = wm * G::WTM + tm * MF + rr;  // row within the tile: rows >= M lie past the range
+            const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
+            const uint32_t off = (uint32_t)(r * p.ldc + n) * OSZ;
+            buf_store16(rc, n < p.N ? off : ICPP_OOB_OFFSET, v);
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    };
+
+    if constexpr (EPI == EPI_STORE) {
+      if (p.partial) {
+        float* ws = p.ws + (size_t)kz * p.M * p.N;
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          const int m = out_row(tm);
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+              const int n = out_col(tn, g);
+              if (m < p.M && n < p.N) Vec4Store<float>::st(ws + (size_t)m * p.N + n, get4(tm, tn, g));
+            }
+        }
+      } else {
+        const BiasT* bias = (const BiasT*)p.bias;
+        f32x4 bv[G::TN][NG];
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const int n = out_col(tn, g);
+            bv[tn][g] = (bias != nullptr && n < p.N) ? Vec4Store<BiasT>::ld(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        dispatch_act(p.act, [&](auto ACT) ICPP_INLINE {
+          store_staged([&](int tm, int tn, int g) ICPP_INLINE {
+            f32x4 v = get4(tm, tn, g);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = act_fn<decltype(ACT)::value>(v[e] * p.alpha + bv[tn][g][e]);
+            return v;
+          });
+        });
+      }
+    } else {
+      // LayerNorm epilogues: x = acc + bias, statistics over valid columns (n < N)
+      OutT* C = (OutT*)p.C;
+      const BiasT* bias = (const BiasT*)p.bias;
+      float xs[G::TM][G::TN][Op::ACC];
+#pragma unroll
+      for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int n = out_col(tn, g);
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (bias != nullptr && n < p.N) bv = Vec4Store<BiasT>::ld(bias + n);
+          const bool ok = n < p.N;
+#pragma unroll
+          for (int tm = 0; tm < G::TM; ++tm)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] = ok ? (acc[tm][tn][4 * g + e] + bv[e]) : 0.f;
+        }
+      // row sums over this wave's columns, reduced across the lanes sharing a row
+      auto lane_reduce = [&](float v) ICPP_INLINE {
+        if (MF == 16) {
+          v += __shfl_xor(v, 16);
+          v += __shfl_xor(v, 32);
+        } else {
+          v += __shfl_xor(v, 32);
+        }
+        return v;
+      };
+      const int wcol0 = col0 + wn * G::WTN;
+      const int wcnt = max(0, min(G::WTN, p.N - wcol0));
+      if constexpr (EPI == EPI_LN_STATS) {
+        float* ws = p.ws;
+        const int scol = wcol0 / G::WTN;
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          float s = 0.f;
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int e = 0; e < Op::ACC; ++e) s += xs[tm][tn][e];
+          s = lane_reduce(s);
+          const float mean = wcnt > 0 ? s / (float)wcnt : 0.f;
+          float q = 0.f;
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+              const bool ok = out_col(tn, g) < p.N;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float d = xs[tm][tn][4 * g + e] - mean;
+                q += ok ? d * d : 0.f;
+              }
+            }
+          q = lane_reduce(q);
+          const int m = out_row(tm);
+          if (lane < MF && m < p.M && scol < p.stat_cols) {
+            ws[((size_t)m * p.stat_cols + scol) * 2 + 0] = mean;
+            ws[((size_t)m * p.stat_cols + scol) * 2 + 1] = q;
+          }
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+              const int n = out_col(tn, g);
+              f32x4 v = {xs[tm][tn][4 * g], xs[tm][tn][4 * g + 1], xs[tm][tn][4 * g + 2], xs[tm][tn][4 * g + 3]};
+              if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
+            }
+        }
+      } else {
+        // EPI_LN_ROW: the workgroup owns whole rows (tiles_n == 1, N <= BN); two-pass
+        // mean / centred variance in registers, cross-wave through LDS.
+        __syncthreads();  // mainloop LDS no longer needed
+        static_assert(2 * WN * BM * 4 <= G::STAGE_BYTES, "LN reduction scratch must fit one LDS stage");
+        float ICPP_LDS* red = (float ICPP_LDS*)lds0;       // [WN][BM]
+        float ICPP_LDS* red2 = red + WN * BM;               // [WN][BM]
+        const BiasT* gamma = (const BiasT*)p.gamma;
+        const BiasT* beta = (const BiasT*)p.beta;
+        const float inv_n = 1.f / (float)p.N;
+        float mean[G::TM], rstd[G::TM];
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          float s = 0.f;
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int e = 0; e < Op::ACC; ++e) s += xs[tm][tn][e];
+          s = lane_reduce(s);
+          if (lane < MF) red[wn * BM + wm * G::WTM + tm * MF + lane] = s;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          float s = 0.f;
+          const int lr = wm * G::WTM + tm * MF + (lane % MF);
+#pragma unroll
+          for (int w = 0; w < WN; ++w) s += red[w * BM + lr];
+          mean[tm] = s * inv_n;
+          float q = 0.f;
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+              const bool ok = out_col(tn, g) < p.N;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float d = xs[tm][tn][4 * g + e] - mean[tm];
+                q += ok ? d * d : 0.f;
+              }
+            }
+          q = lane_reduce(q);
+          if (lane < MF) red2[wn * BM + lr] = q;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          float q = 0.f;
+          const int lr = wm * G::WTM + tm * MF + (lane % MF);
+#pragma unroll
+          for (int w = 0; w < WN; ++w) q += red2[w * BM + lr];
+          rstd[tm] = rsqrtf(q * inv_n + p.eps);
+        }
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const int n = out_col(tn, g);
+            if (n >= p.N) continue;
+            const f32x4 gv = Vec4Store<BiasT>::ld(gamma + n);
+            const f32x4 bv = Vec4Store<BiasT>::ld(beta + n);
+#pragma unroll
+            for (int tm = 0; tm < G::TM; ++tm) {
+              const int m = out_row(tm);
+              f32x4 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = (xs[tm][tn][4 * g + e] - mean[tm]) * rstd[tm] * gv[e] + bv[e];
+              if (m < p.M) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
+            }
+          }
+      }
+    }
+  };
+
+  // Issue cursor: the K tile issued last.  Past the last tile it stays there (a
+  // cached re-read into a stage nobody reads again), so every step issues
+  // exactly LOADS loads.
+  int cur_kt = 0;
+  auto advance_issue = [&]() ICPP_INLINE { cur_kt = min(cur_kt + 1, nk - 1); };
+  auto cur_kk = [&]() ICPP_INLINE { return first.kz * p.k_split + cur_kt * BK; };
+
+  static_for<STAGES>([&](auto S) ICPP_INLINE {
+    if constexpr (decltype(S)::value > 0) advance_issue();
+    issue_tile(cur_kk(), S);
+  });
+  wait_tiles(std::integral_constant<int, STAGES - 1>{});  // this wave's loads of tile 0 landed
   lds_barrier();  // tile 0 published
   load_frags(stage_base(std::integral_constant<int, 0>{}), stage_base(std::integral_constant<int, 0>{}) + G::A_BYTES,
              std::integral_constant<int, 0>{}, fa[0], fb[0]);
   for (int kt0 = 0; kt0 < nk; kt0 += STAGES) {
-    // the stage index of each tile is a compile-time constant: kt0 % STAGES == 0
+    // the stage index of each step is a compile-time constant: kt0 % STAGES == 0
     static_for<STAGES>([&](auto J) ICPP_INLINE {
       constexpr int j = decltype(J)::value;
       const int kt = kt0 + j;
@@ -647,9 +950,10 @@ gemm_kernel(KArgs p) {
             mfma_step(fa[s & 1], fb[s & 1]);
             schedule(std::integral_constant<int, 0>{});
           } else {
-            wait_vmcnt<(STAGES - 2) * LOADS>();  // this wave's loads of tile kt+1 landed
+            advance_issue();                      // cursor -> step kt+STAGES (clamped)
+            wait_tiles(std::integral_constant<int, STAGES - 2>{});  // this wave's loads of tile kt+1 landed
             lds_barrier();                        // B(kt): tile kt+1 published, stage j retired
-            issue_tile(min(kt + STAGES, nk - 1), J);
+            issue_tile(cur_kk(), J);
             constexpr int jn = (j + 1) % STAGES;
             const char ICPP_LDS* an = stage_base(std::integral_constant<int, jn>{});
             load_frags(an, an + G::A_BYTES, std::integral_constant<int, 0>{}, fa[(s + 1) & 1], fb[(s + 1) & 1]);
@@ -661,244 +965,7 @@ gemm_kernel(KArgs p) {
     });
   }
   wait_vmcnt<0>();  // no LDS-DMA write may land after this point (epilogue staging, next workgroup)
-
-  // ---- epilogue ----
-  // lane owns output row (lane % MF) of each MFMA tile and groups of 4 consecutive columns
-  constexpr int NG = Op::ACC / 4;  // column groups per MFMA tile
-  auto out_row = [&](int tm) ICPP_INLINE { return row0 + wm * G::WTM + tm * MF + (lane % MF); };
-  auto out_col = [&](int tn, int g) ICPP_INLINE {
-    return col0 + wn * G::WTN + tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
-  };
-  auto get4 = [&](int tm, int tn, int g) ICPP_INLINE {
-    return f32x4{acc[tm][tn][4 * g + 0], acc[tm][tn][4 * g + 1], acc[tm][tn][4 * g + 2], acc[tm][tn][4 * g + 3]};
-  };
-
-  // Output through LDS: for each MFMA row band (tm) a wave writes its values
-  // (converted to OutT) into a private padded LDS region, then re-reads them as
-  // 16-byte row chunks, so global stores cover whole contiguous row segments
-  // instead of 8-byte pieces of 16 different rows.
-  auto store_staged = [&](auto&& value4) ICPP_INLINE {
-    constexpr int OSZ = (int)sizeof(OutT);
-    constexpr int ROWB_O = G::WTN * OSZ + 16;           // +16 B rotates rows across banks
-    constexpr int REGION = MF * ROWB_O;
-    constexpr int CPR_O = G::WTN * OSZ / 16;             // 16-byte chunks per output row
-    constexpr int CHUNK_ELEMS = 16 / OSZ;
-    constexpr int PER_STAGE = G::STAGE_BYTES / REGION;  // wave regions per stage array
-    static_assert(PER_STAGE * STAGES >= WM * WN, "epilogue staging must fit the LDS stages");
-    static_assert((G::WTN * OSZ) % 16 == 0, "wave tile rows must be whole 16-byte chunks");
-    // store descriptor over this tile's rows (launchers keep BM * ldc * OSZ < 2 GiB)
-    const uint64_t rows = (uint64_t)(p.M > row0 ? min(p.M - row0, BM) : 0);
-    const __amdgpu_buffer_rsrc_t rc = make_rsrc((OutT*)p.C + (size_t)row0 * p.ldc, (uint32_t)(rows * p.ldc * OSZ));
-    const int w_arr = wave / PER_STAGE;
-    char ICPP_LDS* arr = (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
-                       : (w_arr == 2) ? (char ICPP_LDS*)lds2 : (char ICPP_LDS*)lds3;
-    char ICPP_LDS* region = arr + (wave % PER_STAGE) * REGION;
-    __syncthreads();  // every wave is done reading the pipeline stages
-#pragma unroll
-    for (int tm = 0; tm < G::TM; ++tm) {
-#pragma unroll
-      for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const f32x4 v = value4(tm, tn, g);
-          const int lcol = tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
-          Vec4Store<OutT>::st_lds(region + (lane % MF) * ROWB_O + lcol * OSZ, v);
-        }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int q0 = 0; q0 < MF * CPR_O; q0 += 64) {
-        const int q = q0 + lane;
-        if ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O) {
-          const int rr = q / CPR_O, cc = q % CPR_O;
-          const i32x4 v = *(const i32x4 ICPP_LDS*)(region + rr * ROWB_O + cc * 16);
-          const int r = wm * G::WTM + tm * MF + rr;  // row within the tile: rows >= M lie past the range
-          const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
-          const uint32_t off = (uint32_t)(r * p.ldc + n) * OSZ;
-          buf_store16(rc, n < p.N ? off : ICPP_OOB_OFFSET, v);
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-  };
-
-  if constexpr (EPI == EPI_STORE) {
-    if (p.partial) {
-      float* ws = p.ws + (size_t)kz * p.M * p.N;
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm) {
-        const int m = out_row(tm);
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const int n = out_col(tn, g);
-            if (m < p.M && n < p.N) Vec4Store<float>::st(ws + (size_t)m * p.N + n, get4(tm, tn, g));
-          }
-      }
-    } else {
-      const BiasT* bias = (const BiasT*)p.bias;
-      f32x4 bv[G::TN][NG];
-#pragma unroll
-      for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const int n = out_col(tn, g);
-          bv[tn][g] = (bias != nullptr && n < p.N) ? Vec4Store<BiasT>::ld(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      dispatch_act(p.act, [&](auto ACT) ICPP_INLINE {
-        store_staged([&](int tm, int tn, int g) ICPP_INLINE {
-          f32x4 v = get4(tm, tn, g);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = act_fn<decltype(ACT)::value>(v[e] * p.alpha + bv[tn][g][e]);
-          return v;
-        });
-      });
-    }
-  } else {
-    // LayerNorm epilogues: x = acc + bias, statistics over valid columns (n < N)
-    OutT* C = (OutT*)p.C;
-    const BiasT* bias = (const BiasT*)p.bias;
-    float xs[G::TM][G::TN][Op::ACC];
-#pragma unroll
-    for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const int n = out_col(tn, g);
-        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-        if (bias != nullptr && n < p.N) bv = Vec4Store<BiasT>::ld(bias + n);
-        const bool ok = n < p.N;
-#pragma unroll
-        for (int tm = 0; tm < G::TM; ++tm)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] = ok ? (acc[tm][tn][4 * g + e] + bv[e]) : 0.f;
-      }
-    // row sums over this wave's columns, reduced across the lanes sharing a row
-    auto lane_reduce = [&](float v) ICPP_INLINE {
-      if (MF == 16) {
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
-      } else {
-        v += __shfl_xor(v, 32);
-      }
-      return v;
-    };
-    const int wcol0 = col0 + wn * G::WTN;
-    const int wcnt = max(0, min(G::WTN, p.N - wcol0));
-    if constexpr (EPI == EPI_LN_STATS) {
-      float* ws = p.ws;
-      const int scol = wcol0 / G::WTN;
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm) {
-        float s = 0.f;
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-          for (int e = 0; e < Op::ACC; ++e) s += xs[tm][tn][e];
-        s = lane_reduce(s);
-        const float mean = wcnt > 0 ? s / (float)wcnt : 0.f;
-        float q = 0.f;
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const bool ok = out_col(tn, g) < p.N;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float d = xs[tm][tn][4 * g + e] - mean;
-              q += ok ? d * d : 0.f;
-            }
-          }
-        q = lane_reduce(q);
-        const int m = out_row(tm);
-        if (lane < MF && m < p.M && scol < p.stat_cols) {
-          ws[((size_t)m * p.stat_cols + scol) * 2 + 0] = mean;
-          ws[((size_t)m * p.stat_cols + scol) * 2 + 1] = q;
-        }
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const int n = out_col(tn, g);
-            f32x4 v = {xs[tm][tn][4 * g], xs[tm][tn][4 * g + 1], xs[tm][tn][4 * g + 2], xs[tm][tn][4 * g + 3]};
-            if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
-          }
-      }
-    } else {
-      // EPI_LN_ROW: the workgroup owns whole rows (tiles_n == 1, N <= BN); two-pass
-      // mean / centred variance in registers, cross-wave through LDS.
-      __syncthreads();  // mainloop LDS no longer needed
-      static_assert(2 * WN * BM * 4 <= G::STAGE_BYTES, "LN reduction scratch must fit one LDS stage");
-      float ICPP_LDS* red = (float ICPP_LDS*)lds0;       // [WN][BM]
-      float ICPP_LDS* red2 = red + WN * BM;               // [WN][BM]
-      const BiasT* gamma = (const BiasT*)p.gamma;
-      const BiasT* beta = (const BiasT*)p.beta;
-      const float inv_n = 1.f / (float)p.N;
-      float mean[G::TM], rstd[G::TM];
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm) {
-        float s = 0.f;
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-          for (int e = 0; e < Op::ACC; ++e) s += xs[tm][tn][e];
-        s = lane_reduce(s);
-        if (lane < MF) red[wn * BM + wm * G::WTM + tm * MF + lane] = s;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm) {
-        float s = 0.f;
-        const int lr = wm * G::WTM + tm * MF + (lane % MF);
-#pragma unroll
-        for (int w = 0; w < WN; ++w) s += red[w * BM + lr];
-        mean[tm] = s * inv_n;
-        float q = 0.f;
-#pragma unroll
-        for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const bool ok = out_col(tn, g) < p.N;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float d = xs[tm][tn][4 * g + e] - mean[tm];
-              q += ok ? d * d : 0.f;
-            }
-          }
-        q = lane_reduce(q);
-        if (lane < MF) red2[wn * BM + lr] = q;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int tm = 0; tm < G::TM; ++tm) {
-        float q = 0.f;
-        const int lr = wm * G::WTM + tm * MF + (lane % MF);
-#pragma unroll
-        for (int w = 0; w < WN; ++w) q += red2[w * BM + lr];
-        rstd[tm] = rsqrtf(q * inv_n + p.eps);
-      }
-#pragma unroll
-      for (int tn = 0; tn < G::TN; ++tn)
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          const int n = out_col(tn, g);
-          if (n >= p.N) continue;
-          const f32x4 gv = Vec4Store<BiasT>::ld(gamma + n);
-          const f32x4 bv = Vec4Store<BiasT>::ld(beta + n);
-#pragma unroll
-          for (int tm = 0; tm < G::TM; ++tm) {
-            const int m = out_row(tm);
-            f32x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (xs[tm][tn][4 * g + e] - mean[tm]) * rstd[tm] * gv[e] + bv[e];
-            if (m < p.M) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
-          }
-        }
-    }
-  }
+  epilogue(first);
 }
 
 // ---------------------------------------------------------------------------

@@ -14,7 +14,8 @@ struct Instance {
   int epi;
   int aload;
   int wave_tile_n;
-  LaunchFn launch;
+  LaunchFn launch;         // conv instances: the per-tile-tap gather (C % block_k == 0)
+  LaunchFn launch_gather;  // conv instances: the per-chunk gather (any C % 8 == 0); else null
 };
 
 int register_instance(const Instance& inst);
@@ -48,7 +49,13 @@ Instance make_instance(int family, const char* name) {
   in.epi = EPI;
   in.aload = AL;
   in.wave_tile_n = G::WTN;
-  in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>;
+  if constexpr (AL == A_IM2COL) {
+    in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL_TAP>;
+    in.launch_gather = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL>;
+  } else {
+    in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>;
+    in.launch_gather = nullptr;
+  }
   return in;
 }
 

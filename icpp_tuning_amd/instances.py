@@ -88,8 +88,11 @@ class Inst:
             problems.append("LDS overflow")
         if self.stages not in (2, 3, 4):
             problems.append("stages must be 2, 3 or 4")
-        if self.stages > 2 and ((self.bm * self.bk * e // 16) % self.threads or (self.bk * self.bn * e // 16) % self.threads):
-            problems.append("deeper LDS rings need the tile loads to divide evenly over the threads")
+        if (self.stages * (self.bk // kf)) % 2:
+            problems.append("stages x MFMA K-steps per tile must be even (fragment double buffer)")
+        loads = -(-(self.bm * self.bk * e // 16) // self.threads) - (-(self.bk * self.bn * e // 16) // self.threads)
+        if loads * (self.stages - 1) >= 64:
+            problems.append("too many loads in flight for vmcnt")
         if problems:
             raise ValueError(f"{self.name}: " + "; ".join(problems))
 
@@ -98,14 +101,13 @@ def _g(dtype, bm, bn, bk, wm, wn, mf, st=2, fam="gemm"):
     return Inst(fam, dtype, bm, bn, bk, wm, wn, mf, st)
 
 
+# 4-wave 256x256 tiles (128x128 per wave) are left out: 256 accumulator
+# registers per lane plus double-buffered fragments spill to scratch.
 def _gemm_tiles(dtype: str) -> List[Inst]:
     return [
-        _g(dtype, 256, 256, 64, 2, 2, 32),
-        _g(dtype, 256, 256, 64, 2, 2, 16),
         _g(dtype, 256, 256, 64, 2, 4, 32),
         _g(dtype, 256, 256, 64, 2, 4, 16),
         _g(dtype, 256, 256, 32, 2, 4, 32, st=4),
-        _g(dtype, 256, 256, 32, 2, 2, 32, st=4),
         _g(dtype, 256, 128, 64, 2, 2, 32, st=3),
         _g(dtype, 128, 256, 64, 2, 2, 32, st=3),
         _g(dtype, 256, 128, 64, 2, 2, 32),
@@ -118,13 +120,21 @@ def _gemm_tiles(dtype: str) -> List[Inst]:
         _g(dtype, 32, 128, 64, 1, 4, 16),
         _g(dtype, 16, 128, 64, 1, 4, 16),
         _g(dtype, 16, 64, 128, 1, 4, 16),
+        # deeper rings and 8-wave mid-size tiles
+        _g(dtype, 256, 128, 64, 2, 4, 16),
+        _g(dtype, 128, 256, 64, 2, 4, 16),
+        _g(dtype, 128, 128, 64, 2, 2, 16, st=3),
+        _g(dtype, 128, 128, 32, 2, 2, 16, st=4),
+        _g(dtype, 64, 128, 64, 1, 4, 16, st=4),
+        _g(dtype, 64, 64, 64, 2, 2, 16, st=4),
+        _g(dtype, 32, 128, 64, 1, 4, 16, st=4),
+        _g(dtype, 16, 128, 64, 1, 4, 16, st=4),
     ]
 
 
 def _fp8_tiles() -> List[Inst]:
     d = "fp8"
     return [
-        _g(d, 256, 256, 128, 2, 2, 32),
         _g(d, 256, 256, 128, 2, 4, 32),
         _g(d, 256, 256, 64, 2, 4, 32, st=4),
         _g(d, 256, 128, 128, 2, 2, 32),
@@ -134,6 +144,12 @@ def _fp8_tiles() -> List[Inst]:
         _g(d, 32, 128, 128, 1, 4, 16),
         _g(d, 16, 128, 256, 1, 4, 16),
         _g(d, 16, 256, 128, 1, 4, 16),
+        # deeper rings / one-shot K for skinny (decode) shapes
+        _g(d, 128, 128, 128, 2, 2, 16, st=4),
+        _g(d, 64, 128, 128, 1, 4, 16, st=4),
+        _g(d, 32, 128, 256, 1, 4, 16, st=3),
+        _g(d, 16, 256, 128, 1, 4, 16, st=4),
+        _g(d, 16, 128, 512, 1, 4, 16),
     ]
 
 
@@ -141,16 +157,19 @@ def _ln_tiles() -> List[Inst]:
     st = "gemm_ln_stats"
     row = "gemm_ln_row"
     return [
-        _g("f16", 256, 256, 64, 2, 2, 32, fam=st),
         _g("f16", 256, 128, 64, 2, 2, 32, fam=st),
         _g("f16", 128, 256, 64, 2, 2, 32, fam=st),
         _g("f16", 128, 128, 64, 2, 2, 32, fam=st),
         _g("f16", 128, 128, 64, 2, 2, 16, fam=st),
+        _g("f16", 256, 256, 64, 2, 4, 16, fam=st),
+        _g("f16", 256, 256, 64, 2, 4, 32, fam=st),
+        _g("f16", 128, 256, 64, 2, 4, 16, fam=st),
+        _g("f16", 128, 128, 64, 2, 2, 16, st=3, fam=st),
+        _g("f16", 128, 128, 32, 2, 2, 16, st=4, fam=st),
         _g("f16", 32, 768, 32, 1, 8, 16, fam=row),
         _g("f16", 64, 768, 32, 1, 8, 16, fam=row),
         _g("f16", 32, 1024, 32, 1, 8, 16, fam=row),
         _g("f16", 64, 1024, 32, 1, 8, 16, fam=row),
-        _g("f16", 64, 1024, 32, 2, 4, 32, fam=row),
     ]
 
 
@@ -165,6 +184,12 @@ def _conv_tiles() -> List[Inst]:
         _g("f16", 128, 128, 64, 2, 2, 16, fam=c),
         _g("f16", 64, 128, 64, 1, 4, 16, fam=c),
         _g("f16", 64, 64, 64, 2, 2, 16, fam=c),
+        _g("f16", 128, 64, 64, 2, 2, 16, st=4, fam=c),
+        _g("f16", 64, 64, 64, 2, 2, 16, st=4, fam=c),
+        _g("f16", 128, 128, 64, 2, 2, 16, st=3, fam=c),
+        _g("f16", 128, 128, 32, 2, 2, 16, st=4, fam=c),
+        _g("f16", 64, 128, 64, 1, 4, 16, st=4, fam=c),
+        _g("f16", 256, 128, 64, 2, 4, 16, fam=c),
     ]
 
 

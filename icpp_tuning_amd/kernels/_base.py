@@ -119,7 +119,12 @@ def compiled_resources(inst: Inst) -> Dict[str, int]:
 
 
 def instance_vgprs(inst: Inst) -> int:
+    """Registers per lane (VGPRs rounded to the allocation granule + AGPRs).  An
+    instance that spilled to scratch needed more than the register file held:
+    it reports the whole file plus one, so the L2 register prune rejects it."""
     r = compiled_resources(inst)
     if not r:
         return 0
+    if r.get("scratch", 0) > 0:
+        return 513
     return -(-(r.get("vgprs", 0)) // 8) * 8 + r.get("agprs", 0)

@@ -48,8 +48,9 @@ def test_resources_recorded_for_every_instance():
     for i in INSTANCES:
         r = res[i.name]
         # pipeline stages plus the 16-byte placeholders of unused stage arrays
-        assert i.lds_bytes <= r["lds"] <= i.lds_bytes + 64
+        assert i.lds_bytes <= r["lds"] <= i.lds_bytes + 64, (i.name, r["lds"])
         assert r["vgprs"] + r["agprs"] <= 512
+        assert r["scratch"] == 0, i.name
 
 
 def test_workspace_bytes(L):

@@ -192,6 +192,26 @@ def test_config5_fp8(gpu, M, NK):
     _close(y, ref, 1e-2, 1e-2, f"config5 M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("shape,sk", [((32, 56, 56, 64, 64), 1), ((32, 14, 14, 256, 256), 2)])
+def test_conv_every_instance_full_size(gpu, shape, sk):
+    """Every conv tile at two benchmark sizes (many workgroup rounds for the small
+    tiles), alone and with split-K."""
+    Nb, H, W, C, F = shape
+    d = I.config4(Nb, H, W, C, F)
+    ref = O.conv2d_nhwc_ref(d["X"], d["W"], 1, 1)
+    X, Wt = d["X"].cuda(), d["W"].cuda()
+    for inst in family_instances("conv2d"):
+        if (9 * C) % (inst.bk * sk):
+            continue
+        raw = raw_from_inst(inst, sk)
+        print(f"[parity] {inst.name} {shape} sk={sk}", flush=True)
+        k = conv_mod.build_conv2d_kernel(Nb, C, H, W, F, 3, 3, 1, 1, 1, config=raw)
+        Y = torch.full((Nb, H, W, F), float("nan"), dtype=torch.float16, device="cuda")
+        k(X, Wt, Y)
+        torch.cuda.synchronize()
+        _close(Y, ref, 1e-2, 1e-2, f"{inst.name} {shape} sk={sk}")
+
+
 @pytest.mark.parametrize("geom", [
     # (N, H, W, C, F, KH, KW, stride, pad, dilation)
     (2, 7, 6, 16, 64, 2, 2, 1, 0, 1),    # K tile spans 4 filter taps (general gather path)
