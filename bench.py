@@ -118,7 +118,7 @@ def bench_ops(quick: bool):
     top_k = 2 if quick else 4
 
     def record(op, desc, shape, flops, min_bytes, dtype, **extra):
-        res = tune(desc, top_k=top_k, warmup=2, reps=5, **shape)
+        res = tune(desc, top_k=top_k, warmup=2, reps=10, budget_ms=60.0, **shape)
         # Timed over input copies whose total exceeds the 256 MiB MALL + L2, so
         # every launch reads its operands from HBM.
         copies = max(1, min(16, -(-(600 << 20) // max(1, min_bytes))))

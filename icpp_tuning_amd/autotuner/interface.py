@@ -195,11 +195,15 @@ def benchmark_ms(fn, warmup: int = 3, reps: int = 10, batches: int = 3, graph: b
 
 
 def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: int = 4, warmup: int = 2,
-         reps: int = 5, **shape_kwargs: Any) -> TuneResult:
-    """Formula-rank, then measure the top-k on the device and keep the fastest.
+         reps: int = 5, budget_ms: float = 0.0, **shape_kwargs: Any) -> TuneResult:
+    """Formula-rank, then measure candidates on the device and keep the fastest.
+
+    The formula's top_k are always measured.  With ``budget_ms`` the search goes
+    on down the ranking while the device time spent measuring stays within the
+    budget, so cheap (small) problems get a wider search than large ones.
 
     time_to_best = prune+rank (host) + compile (instance lookup: kernels are AOT)
-    + top-k device benchmark.  Generating the synthetic inputs is reported
+    + device benchmarks.  Generating the synthetic inputs is reported
     separately (inputs_s) and not counted.
     """
     t0 = time.perf_counter()
@@ -212,14 +216,22 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     t1 = time.perf_counter()
     inputs = descriptor.make_inputs(**shape_kwargs)   # benchmark harness, not tuner work
     t_in = time.perf_counter()
-    runners = [(e, descriptor.make_runner(e["raw_config"], inputs, **shape_kwargs)) for e in ranked[:top_k]]
-    t2 = time.perf_counter()
+    compile_s = 0.0
     flops = descriptor.flops(**shape_kwargs)
     cands = []
-    for e, run in runners:
+    spent_ms = 0.0
+    launches = max(warmup, 1) + 3 * reps + reps       # warmup + 3 timed batches + graph capture
+    for rank, e in enumerate(ranked):
+        if rank >= top_k and spent_ms >= budget_ms:
+            break
+        tc = time.perf_counter()
+        run = descriptor.make_runner(e["raw_config"], inputs, **shape_kwargs)
+        compile_s += time.perf_counter() - tc
         ms = benchmark_ms(run, warmup=warmup, reps=reps)
+        spent_ms += ms * launches
         cands.append({"config": e["raw_config"], "formatted": e["formatted"], "score": e["score"], "ms": ms,
                       "tflops": flops / ms / 1e9})
+    t2 = t_in + compile_s
     t3 = time.perf_counter()
     best = min(cands, key=lambda c: c["ms"])
     return TuneResult(

@@ -75,6 +75,15 @@ hipError_t launch_splitk_reduce(int dt, const float* ws, void* C, const void* bi
   return hipGetLastError();
 }
 
+// Split the nkt K tiles of a problem over at most `split_k` slices of
+// ceil(nkt / split_k) tiles each (the last one may be shorter, none is empty).
+// Returns the number of slices; *k_split receives the K elements per slice.
+int plan_splits(int nkt, int block_k, int split_k, int* k_split) {
+  const int per = ceil_div(nkt, split_k);
+  *k_split = per * block_k;
+  return ceil_div(nkt, per);
+}
+
 KArgs base_args() {
   KArgs a;
   memset(&a, 0, sizeof(a));
@@ -145,8 +154,9 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
   if (N % 8 || lda % vec || ldb % vec || ldc % 8 || lda < K || ldb < N || ldc < N)
     return fail(ICPP_E_SHAPE, "icpp_gemm: need N%%8==0, lda,ldb multiples of %d, ldc%%8==0 (N=%d lda=%d ldb=%d ldc=%d)",
                 vec, N, lda, ldb, ldc);
-  if (K % (t.block_k * split_k))
-    return fail(ICPP_E_SHAPE, "icpp_gemm: K=%d not a multiple of block_k*split_k=%d", K, t.block_k * split_k);
+  if (K % t.block_k || split_k > K / t.block_k)
+    return fail(ICPP_E_SHAPE, "icpp_gemm: K=%d must be a multiple of block_k=%d with at least split_k=%d K tiles", K,
+                t.block_k, split_k);
   if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias)))
     return fail(ICPP_E_ARG, "icpp_gemm: pointers must be 16-byte aligned");
   if ((uint64_t)t.block_m * lda * e > 0x7FFFFFFFull || (uint64_t)K * ldb * e > 0xFFFFFFF0ull ||
@@ -156,13 +166,12 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
   a.A = A; a.B = B; a.bias = bias; a.C = C;
   a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
   a.act = act; a.alpha = scale_a * scale_b;
-  a.k_split = K / split_k;
-  a.splits = split_k;
+  a.splits = plan_splits(K / t.block_k, t.block_k, split_k, &a.k_split);
   a.tiles_m = ceil_div(M, t.block_m);
   a.tiles_n = ceil_div(N, t.block_n);
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(a.tiles_m * a.tiles_n * split_k);  // one workgroup per (tile, K split) item
-  if (split_k > 1) {
+  const dim3 grid(a.tiles_m * a.tiles_n * a.splits);  // one workgroup per (tile, K split) item
+  if (a.splits > 1) {
     const size_t need = (size_t)split_k * M * N * sizeof(float);
     if (!workspace || ws_bytes < need || !aligned16(workspace))
       return fail(ICPP_E_WORKSPACE, "icpp_gemm: split_k=%d needs %zu workspace bytes (got %zu)", split_k, need, ws_bytes);
@@ -171,7 +180,7 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
     a.ws = (float*)workspace;
     int rc = check_launch(in->launch(a, grid, s), t.name);
     if (rc) return rc;
-    return check_launch(launch_splitk_reduce(t.dtype, a.ws, C, bias, M, N, ldc, split_k, a.alpha, act, s), "splitk_reduce");
+    return check_launch(launch_splitk_reduce(t.dtype, a.ws, C, bias, M, N, ldc, a.splits, a.alpha, act, s), "splitk_reduce");
   }
   return check_launch(in->launch(a, grid, s), t.name);
 }
@@ -234,8 +243,9 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   if (C % 8 || F % 8) return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: need C%%8==0 and F%%8==0 (C=%d F=%d)", C, F);
   const long long Mg = (long long)N * OH * OW;
   const long long Kg = (long long)KH * KW * C;
-  if (Mg > 0x7FFFFFFF || Kg % ((long long)t.block_k * split_k))
-    return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: K=%lld not a multiple of block_k*split_k=%d", Kg, t.block_k * split_k);
+  if (Mg > 0x7FFFFFFF || Kg % t.block_k || split_k > Kg / t.block_k)
+    return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: K=%lld must be a multiple of block_k=%d with at least split_k=%d K tiles",
+                Kg, t.block_k, split_k);
   const unsigned long long xbytes = (unsigned long long)N * H * W * C * 2;
   // padding taps load from offset xbytes (past the range): keep it and the output block rows below 2 GiB
   if (xbytes > 0x7FFFFFF0ull || (uint64_t)t.block_m * F * 2 > 0x7FFFFFFFull)
@@ -244,8 +254,7 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   KArgs a = base_args();
   a.A = X; a.B = Wt; a.C = Y;
   a.M = (int)Mg; a.N = F; a.K = (int)Kg; a.lda = 0; a.ldb = F; a.ldc = F;
-  a.k_split = (int)Kg / split_k;
-  a.splits = split_k;
+  a.splits = plan_splits((int)(Kg / t.block_k), t.block_k, split_k, &a.k_split);
   a.tiles_m = ceil_div(a.M, t.block_m);
   a.tiles_n = ceil_div(F, t.block_n);
   a.cH = H; a.cW = W; a.cC = C; a.cKH = KH; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH;
@@ -254,8 +263,8 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   hipStream_t s = (hipStream_t)stream;
   // every K tile inside one filter tap (and the tap set fits the 64-bit mask): per-tile-tap gather
   const LaunchFn launch = (C % t.block_k == 0 && KH * KW <= 64) ? in->launch : in->launch_gather;
-  const dim3 grid(a.tiles_m * a.tiles_n * split_k);  // one workgroup per (tile, K split) item
-  if (split_k > 1) {
+  const dim3 grid(a.tiles_m * a.tiles_n * a.splits);  // one workgroup per (tile, K split) item
+  if (a.splits > 1) {
     const size_t need = (size_t)split_k * a.M * F * sizeof(float);
     if (!workspace || ws_bytes < need || !aligned16(workspace))
       return fail(ICPP_E_WORKSPACE, "icpp_conv2d_nhwc: split_k=%d needs %zu workspace bytes (got %zu)", split_k, need, ws_bytes);
@@ -263,7 +272,7 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
     a.ws = (float*)workspace;
     int rc = check_launch(launch(a, grid, s), t.name);
     if (rc) return rc;
-    return check_launch(launch_splitk_reduce(DT_F16, a.ws, Y, nullptr, a.M, F, F, split_k, 1.f, ICPP_ACT_NONE, s), "splitk_reduce");
+    return check_launch(launch_splitk_reduce(DT_F16, a.ws, Y, nullptr, a.M, F, F, a.splits, 1.f, ICPP_ACT_NONE, s), "splitk_reduce");
   }
   return check_launch(launch(a, grid, s), t.name);
 }

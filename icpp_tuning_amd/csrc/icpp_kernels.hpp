@@ -72,7 +72,7 @@ struct KArgs {
   int act;
   float alpha;        // scale_a * scale_b (fp8), 1 otherwise
   float eps;
-  int k_split;        // K elements per split slice (multiple of BK); K == splits * k_split
+  int k_split;        // K elements per split slice (multiple of BK); the last slice may be shorter
   int splits;         // K slices (split-K); items = tiles_m * tiles_n * splits
   int tiles_m, tiles_n;
   int stat_cols;      // LN stats columns per row
@@ -385,8 +385,8 @@ gemm_kernel(KArgs p) {
     const int gm = min(p.tiles_m - first_m, GROUP);
     return Item{(first_m + (t % group_size) % gm) * BM, ((t % group_size) / gm) * BN, kz};
   };
-  const int nk = p.k_split / BK;  // K tiles of the item
   const Item first = item_of(slot);
+  const int nk = min(p.k_split, p.K - first.kz * p.k_split) / BK;  // K tiles of the item (>= 1)
 
   // ---- global -> LDS: buffer_load_dwordx4 ... lds (16 B per lane, range-checked:
   // out-of-range lanes deliver zeros).  Load i of wave w writes LDS chunks

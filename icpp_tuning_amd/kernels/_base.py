@@ -73,7 +73,17 @@ class InstanceDescriptor(TileLangKernelBase):
         return shape["K"]
 
     def shape_ok(self, inst: Inst, split_k: int, **shape) -> bool:
-        return self.k_extent(**shape) % (inst.bk * split_k) == 0
+        """K a whole number of tiles, and split_k slices of ceil(tiles / split_k)
+        tiles each are all non-empty (the launcher's split plan uses exactly
+        split_k slices), so distinct split_k values are distinct launches."""
+        k = self.k_extent(**shape)
+        if k % inst.bk:
+            return False
+        nkt = k // inst.bk
+        if split_k > nkt:
+            return False
+        per = -(-nkt // split_k)
+        return -(-nkt // per) == split_k
 
     def get_raw_configs(self, **shape_kwargs: Any) -> List[Dict[str, Any]]:
         out = []

@@ -33,7 +33,7 @@ def calc_conv_flops(N, C, OH, OW, F_out, KH, KW):
 class Conv2dDescriptor(InstanceDescriptor):
     family = "conv2d"
     dtype = "f16"
-    split_k_values = (1, 2, 4)
+    split_k_values = (1, 2, 4, 8)
 
     @property
     def name(self) -> str:

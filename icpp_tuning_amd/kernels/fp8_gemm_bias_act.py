@@ -22,7 +22,7 @@ from .gemm import CompiledGemm
 class Fp8GemmBiasActDescriptor(InstanceDescriptor):
     family = "gemm"
     dtype = "fp8"
-    split_k_values = (1, 2, 4, 8)
+    split_k_values = (1, 2, 4, 8, 16)
 
     def __init__(self, act: str = "silu"):
         super().__init__("fp8")

@@ -75,6 +75,7 @@ def test_validation_errors_before_launch(L):
     assert _gemm_call(L, K=40) == -2           # K not a multiple of block_k
     assert _gemm_call(L, act=9) == -4
     assert _gemm_call(L, split=2, K=256) == -3  # split-K without workspace
+    assert _gemm_call(L, split=64, K=256) == -2  # more slices than K tiles
     assert _gemm_call(L, A=17) == -4           # misaligned pointer
     assert "aligned" in L.last_error()
     f = L._dll.icpp_gemm_bias_layernorm

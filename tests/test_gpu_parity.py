@@ -192,6 +192,38 @@ def test_config5_fp8(gpu, M, NK):
     _close(y, ref, 1e-2, 1e-2, f"config5 M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("dtype,M,N,K,sk", [("fp8", 16, 512, 11008, 4), ("fp8", 40, 256, 11008, 8),
+                                            ("f16", 61, 384, 11008, 8), ("bf16", 7, 256, 1216, 3)])
+def test_uneven_split_k(gpu, dtype, M, N, K, sk):
+    """split_k slices of ceil(K tiles / split_k) tiles, the last one shorter
+    (K = 11008 = 86 x 128 = 172 x 64 tiles; 1216 = 19 x 64), every instance whose
+    split plan is exactly sk slices."""
+    from icpp_tuning_amd.kernels._base import InstanceDescriptor  # noqa: F401
+    if dtype == "fp8":
+        d = I.config5(M, N, K)
+        ref = O.fp8_gemm_bias_act_ref(d["A"], d["B"], d["scale_a"], d["scale_b"], d["bias"], "silu")
+        args = dict(act="silu", scale_a=d["scale_a"], scale_b=d["scale_b"])
+    else:
+        d = I.gemm_inputs(M, N, K, runtime.TORCH_DTYPE[dtype], 97, b_std=1 / math.sqrt(K), bias=True)
+        ref = O.gemm_bias_act_ref(d["A"], d["B"], d["bias"], "relu")
+        args = dict(act="relu")
+    A, B, bias = d["A"].cuda(), d["B"].cuda(), d["bias"].cuda()
+    ran = 0
+    for idx, inst in enumerate(family_instances("gemm")):
+        if inst.dtype != dtype or K % inst.bk:
+            continue
+        nkt = K // inst.bk
+        per = -(-nkt // sk)
+        if sk > nkt or -(-nkt // per) != sk or nkt % per == 0:
+            continue  # only plans whose last slice is shorter
+        print(f"[parity] {inst.name} M={M} N={N} K={K} sk={sk}", flush=True)
+        y = runtime.gemm(idx, dtype, A, B, bias=bias, split_k=sk, **args)
+        torch.cuda.synchronize()
+        _close(y, ref, 1e-2, 1e-2, f"{inst.name} uneven sk={sk}")
+        ran += 1
+    assert ran > 0
+
+
 @pytest.mark.parametrize("shape,sk", [((32, 56, 56, 64, 64), 1), ((32, 14, 14, 256, 256), 2)])
 def test_conv_every_instance_full_size(gpu, shape, sk):
     """Every conv tile at two benchmark sizes (many workgroup rounds for the small
