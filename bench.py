@@ -103,7 +103,7 @@ def _load_traffic(workload: str):
         return None
 
 
-def bench_ops(quick: bool):
+def bench_ops(quick: bool, only: str = ""):
     """Every benchmark configuration: tuned config, TFLOP/s, fraction of its roofline."""
     import torch
 
@@ -118,6 +118,8 @@ def bench_ops(quick: bool):
     top_k = 2 if quick else 4
 
     def record(op, desc, shape, flops, min_bytes, dtype, **extra):
+        if only and not op.startswith(only):
+            return
         res = tune(desc, top_k=top_k, warmup=2, reps=10, budget_ms=60.0, **shape)
         # Timed over input copies whose total exceeds the 256 MiB MALL + L2, so
         # every launch reads its operands from HBM.
@@ -183,6 +185,8 @@ def main():
                     help="tune + time the headline kernel only (for profiler runs)")
     ap.add_argument("--instance", default=None,
                     help="time this compiled GEMM instance (by name) instead of the tuned one")
+    ap.add_argument("--op", default="",
+                    help="per-op table only, for the ops whose name starts with this (e.g. conv2d, gemm_bias_layernorm)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -211,6 +215,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
+    if args.op:  # one family of per-op rows only (profiling runs)
+        print(json.dumps({"ops": bench_ops(args.quick, args.op)}), flush=True)
+        return 0
     M = N = K = 4096
     desc = GBA.descriptor("gelu_tanh", "bf16")
     t_sel = time.perf_counter()
