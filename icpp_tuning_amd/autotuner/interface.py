@@ -109,11 +109,13 @@ def select_best(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None,
 
 
 def rank_all(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, detailed: bool = False,
-             **shape_kwargs: Any) -> List[Dict[str, Any]]:
-    """Every (pruned) config with its score, best first (stable sort)."""
+             prune: bool = True, **shape_kwargs: Any) -> List[Dict[str, Any]]:
+    """Every (pruned, unless prune=False) config with its score, best first (stable sort)."""
     if hw is None:
         hw = get_gpu_spec()
-    configs = descriptor.prune(descriptor.get_raw_configs(**shape_kwargs), hw, **shape_kwargs)
+    configs = descriptor.get_raw_configs(**shape_kwargs)
+    if prune:
+        configs = descriptor.prune(configs, hw, **shape_kwargs)
     out = []
     for raw in configs:
         s, detail = _score(descriptor, raw, hw, detailed, shape_kwargs)
@@ -195,12 +197,14 @@ def benchmark_ms(fn, warmup: int = 3, reps: int = 10, batches: int = 3, graph: b
 
 
 def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: int = 4, warmup: int = 2,
-         reps: int = 5, budget_ms: float = 0.0, **shape_kwargs: Any) -> TuneResult:
+         reps: int = 5, budget_ms: float = 0.0, prune: bool = True, **shape_kwargs: Any) -> TuneResult:
     """Formula-rank, then measure candidates on the device and keep the fastest.
 
     The formula's top_k are always measured.  With ``budget_ms`` the search goes
     on down the ranking while the device time spent measuring stays within the
     budget, so cheap (small) problems get a wider search than large ones.
+    ``prune=False`` ranks (and, with a large top_k, measures) the whole compiled
+    set for the shape, as offline profiling does.
 
     time_to_best = prune+rank (host) + compile (instance lookup: kernels are AOT)
     + device benchmarks.  Generating the synthetic inputs is reported
@@ -210,7 +214,7 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     if hw is None:
         hw = get_gpu_spec()
     all_cfgs = descriptor.get_raw_configs(**shape_kwargs)
-    ranked = rank_all(descriptor, hw, **shape_kwargs)
+    ranked = rank_all(descriptor, hw, prune=prune, **shape_kwargs)
     if not ranked:
         raise RuntimeError(f"No configs survive pruning for {descriptor.name} with {shape_kwargs}")
     t1 = time.perf_counter()

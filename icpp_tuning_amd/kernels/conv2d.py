@@ -16,7 +16,7 @@ from typing import Any, Dict, Optional
 import torch
 
 from ..autotuner.cost_model import make_conv2d_spec
-from ..autotuner.interface import select_best
+from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from .. import runtime
 from ._base import InstanceDescriptor
@@ -107,7 +107,7 @@ class CompiledConv2d:
 
 def build_conv2d_kernel(N, C, H, W, F_out, KH, KW, S=1, P=1, D=1, config=None):
     if config is None:
-        config, _ = select_best(DESCRIPTOR, N=N, C=C, H=H, W=W, OC=F_out, KH=KH, KW=KW, stride=S, padding=P)
+        config = select_config(DESCRIPTOR, N=N, C=C, H=H, W=W, OC=F_out, KH=KH, KW=KW, stride=S, padding=P)
     return CompiledConv2d(N, C, H, W, F_out, KH, KW, S, P, D, config)
 
 

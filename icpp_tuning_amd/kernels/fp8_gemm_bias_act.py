@@ -13,7 +13,7 @@ import torch
 
 from ..autotuner.cost_model import ACT_PRIMITIVE, make_matmul_spec
 from ..autotuner.gpu_spec import get_gpu_spec
-from ..autotuner.interface import select_best
+from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from ._base import InstanceDescriptor
 from .gemm import CompiledGemm
@@ -73,7 +73,7 @@ class CompiledFp8Gemm(CompiledGemm):
 def build_kernel(M, N, K, config=None, act: str = "silu"):
     d = DESCRIPTOR if act == "silu" else Fp8GemmBiasActDescriptor(act)
     if config is None:
-        config, _ = select_best(d, M=M, N=N, K=K)
+        config = select_config(d, M=M, N=N, K=K)
     return CompiledFp8Gemm(d, M, N, K, config, act=act)
 
 

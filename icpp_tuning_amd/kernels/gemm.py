@@ -16,7 +16,7 @@ import torch
 
 from ..autotuner.cost_model import make_matmul_spec
 from ..autotuner.gpu_spec import get_gpu_spec
-from ..autotuner.interface import select_best
+from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from .. import runtime
 from ._base import InstanceDescriptor
@@ -90,9 +90,10 @@ class CompiledGemm:
 
 
 def build_kernel(M, N, K, config=None):
-    """Resolve a config (cost-model top-1 when None) to its compiled instance."""
+    """Resolve a config to its compiled instance; None selects one (the shipped
+    measured table for profiled shape ranges, else the cost model's top-1)."""
     if config is None:
-        config, _ = select_best(DESCRIPTOR, M=M, N=N, K=K)
+        config = select_config(DESCRIPTOR, M=M, N=N, K=K)
     return CompiledGemm(DESCRIPTOR, M, N, K, config)
 
 

@@ -14,7 +14,7 @@ import math
 import torch
 
 from ..autotuner.cost_model import ACT_PRIMITIVE, make_matmul_spec
-from ..autotuner.interface import select_best
+from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from ._base import InstanceDescriptor
 from .gemm import CompiledGemm
@@ -65,10 +65,11 @@ def get_configs(M, K, dtype: str = "bf16", N: int = 0):
 
 
 def build_kernel(M, N, K, config=None, act: str = "relu", dtype: str = "bf16"):
-    """``kernel(a, b, bias) -> act(a @ b + bias)``; config=None selects by cost model."""
+    """``kernel(a, b, bias) -> act(a @ b + bias)``; config=None selects one (the shipped
+    measured table for profiled shape ranges, else the cost model's top-1)."""
     d = descriptor(act, dtype)
     if config is None:
-        config, _ = select_best(d, M=M, N=N, K=K)
+        config = select_config(d, M=M, N=N, K=K)
     return CompiledGemm(d, M, N, K, config, act=act)
 
 

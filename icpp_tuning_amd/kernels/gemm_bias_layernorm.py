@@ -22,7 +22,7 @@ from typing import Any, Dict, List, Optional
 import torch
 
 from ..autotuner.cost_model import make_matmul_spec
-from ..autotuner.interface import select_best
+from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from .. import runtime
 from ._base import InstanceDescriptor, family_instances, raw_from_inst
@@ -122,7 +122,7 @@ def build_fused_kernel(M, N, K, gemm_config=None, block_M_ln=16, block_N_ln=128,
     LayerNorm here is either fused into the GEMM epilogue or a fixed-geometry
     finalize pass (one wave per row)."""
     if gemm_config is None:
-        gemm_config, _ = select_best(DESCRIPTOR, M=M, N=N, K=K)
+        gemm_config = select_config(DESCRIPTOR, M=M, N=N, K=K)
     return CompiledGemmLayerNorm(M, N, K, gemm_config, eps=eps)
 
 
