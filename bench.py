@@ -109,6 +109,7 @@ def bench_ops(quick: bool, only: str = ""):
 
     from icpp_tuning_amd.autotuner.interface import benchmark_ms, tune
     from icpp_tuning_amd.kernels import conv2d as CV
+    from icpp_tuning_amd.kernels import conv2d_fused as CF
     from icpp_tuning_amd.kernels import fp8_gemm_bias_act as F8
     from icpp_tuning_amd.kernels import gemm as G
     from icpp_tuning_amd.kernels import gemm_bias_act as GBA
@@ -165,6 +166,12 @@ def bench_ops(quick: bool, only: str = ""):
         shape = dict(N=Nb, C=C, H=H, W=W, OC=F, KH=3, KW=3, stride=1, padding=1)
         record("conv2d", CV.DESCRIPTOR, shape, float(CV.calc_conv_flops(Nb, C, H, W, F, 3, 3)),
                2 * (Nb * H * W * C + 9 * C * F + Nb * H * W * F), "f16")
+        # fused epilogues (reference conv2d_bn_relu.py / conv_bn_add_relu.py): + BN parameters, + residual read
+        for variant in (["conv2d_bn_relu"] if quick else ["conv2d_bn_relu", "conv_bn_add_relu"]):
+            d = CF.DESCRIPTORS[variant]
+            record(variant, d, shape, d.flops(**shape),
+                   2 * (Nb * H * W * C + 9 * C * F + Nb * H * W * F + 4 * F + (Nb * H * W * F if d.residual else 0)),
+                   "f16")
     f8_shapes = [(16, 4096, 4096), (4096, 4096, 4096)] if quick else [
         (m, n, k) for m in (16, 256, 4096) for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008))]
     for (M, N, K) in f8_shapes:

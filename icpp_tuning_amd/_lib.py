@@ -27,8 +27,9 @@ ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu": 2, "silu": 3}
 # every symbol declared in include/icpp_hip.h
 EXPORTED_SYMBOLS = (
     "icpp_abi_version", "icpp_last_error", "icpp_num_instances", "icpp_instance_info",
-    "icpp_workspace_bytes", "icpp_gemm", "icpp_gemm_bias_layernorm", "icpp_conv2d_nhwc",
+    "icpp_workspace_bytes", "icpp_gemm", "icpp_gemm_bias_layernorm", "icpp_conv2d_nhwc", "icpp_conv2d_nhwc_fused",
 )
+CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
 
 class IcppLibraryError(RuntimeError):
@@ -61,6 +62,8 @@ _SIGNATURES = {
     "icpp_gemm": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp, _sz, _vp]),
     "icpp_gemm_bias_layernorm": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp]),
     "icpp_conv2d_nhwc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "icpp_conv2d_nhwc_fused": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i,
+                                    _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
 }
 
 

@@ -366,7 +366,7 @@ def held_out(shapes: Sequence[Dict[str, int]], axis: Optional[str] = None) -> Li
 def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
     """The shapes the shipped databases were profiled on."""
     hw = hw or get_gpu_spec()
-    if op == "conv2d":
+    if op == "conv2d" or op.startswith("conv2d_") or op == "conv_bn_add_relu":
         geos = [dict(C=64, H=56, W=56, OC=64, KH=3, KW=3, stride=1, padding=1),
                 dict(C=256, H=14, W=14, OC=256, KH=3, KW=3, stride=1, padding=1),
                 dict(C=512, H=7, W=7, OC=512, KH=3, KW=3, stride=1, padding=1)]
@@ -385,10 +385,10 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
 
 
 def _descriptors():
-    from ..kernels import conv2d, fp8_gemm_bias_act, gemm, gemm_bias_act, gemm_bias_layernorm
+    from ..kernels import conv2d, conv2d_fused, fp8_gemm_bias_act, gemm, gemm_bias_act, gemm_bias_layernorm
 
     ds = [gemm.DESCRIPTOR, gemm_bias_act.descriptor("gelu_tanh", "bf16"), gemm_bias_layernorm.DESCRIPTOR,
-          fp8_gemm_bias_act.DESCRIPTOR, conv2d.DESCRIPTOR]
+          fp8_gemm_bias_act.DESCRIPTOR, conv2d.DESCRIPTOR] + list(conv2d_fused.DESCRIPTORS.values())
     return {d.name: d for d in ds}
 
 

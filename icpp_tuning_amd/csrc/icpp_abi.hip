@@ -10,6 +10,10 @@
 
 #include "icpp_registry.hpp"
 
+static_assert((int)ICPP_CONV_EPI_BN == (int)icpp::CEPI_BN && (int)ICPP_CONV_EPI_RESIDUAL == (int)icpp::CEPI_RESIDUAL &&
+                  (int)ICPP_CONV_EPI_VAR_CLAMP == (int)icpp::CEPI_VAR_CLAMP,
+              "conv epilogue flags: header and kernels agree");
+
 namespace icpp {
 
 namespace {
@@ -63,15 +67,15 @@ int check_launch(hipError_t e, const char* what) {
 }
 
 hipError_t launch_splitk_reduce(int dt, const float* ws, void* C, const void* bias, int M, int N, int ldc,
-                                int splits, float alpha, int act, hipStream_t s) {
+                                int splits, float alpha, int act, hipStream_t s, ConvEpiArgs ce = ConvEpiArgs{}) {
   const size_t groups = (size_t)M * (N / 4);
   const int blocks = (int)std::min<size_t>((groups + 255) / 256, 4096);
   if (dt == DT_F16)
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act);
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
   else if (dt == DT_BF16)
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act);
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
   else
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT_FP8>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act);
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_FP8>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
   return hipGetLastError();
 }
 
@@ -230,10 +234,33 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
                      int N, int H, int W, int C, int F, int KH, int KW,
                      int stride, int pad, int dilation, int split_k,
                      void* workspace, size_t ws_bytes, void* stream) {
+  return icpp_conv2d_nhwc_fused(inst, X, Wt, Y, nullptr, nullptr, nullptr, nullptr, nullptr, 0.f, 0, ICPP_ACT_NONE,
+                                N, H, W, C, F, KH, KW, stride, pad, dilation, split_k, workspace, ws_bytes, stream);
+}
+
+int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, const void* residual,
+                           const void* gamma, const void* beta, const void* mean, const void* var,
+                           float eps, int epi_flags, int act,
+                           int N, int H, int W, int C, int F, int KH, int KW,
+                           int stride, int pad, int dilation, int split_k,
+                           void* workspace, size_t ws_bytes, void* stream) {
   const Instance* in = lookup(ICPP_FAMILY_CONV2D, inst);
   if (!in) return fail(ICPP_E_INSTANCE, "icpp_conv2d_nhwc: no conv instance %d", inst);
   const icpp_tile_t& t = in->tile;
   if (!X || !Wt || !Y) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: null tensor");
+  if (epi_flags & ~(ICPP_CONV_EPI_BN | ICPP_CONV_EPI_RESIDUAL | ICPP_CONV_EPI_VAR_CLAMP))
+    return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: unknown epilogue flags 0x%x", epi_flags);
+  if (act != ICPP_ACT_NONE && act != ICPP_ACT_RELU)
+    return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: act must be NONE or RELU (got %d)", act);
+  const bool bn = (epi_flags & ICPP_CONV_EPI_BN) != 0;
+  if (bn && (!gamma || !beta || !mean || !var))
+    return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: BN needs gamma, beta, mean and var");
+  if ((epi_flags & ICPP_CONV_EPI_VAR_CLAMP) && !bn) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: VAR_CLAMP without BN");
+  if ((epi_flags & ICPP_CONV_EPI_RESIDUAL) && !residual) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: RESIDUAL needs a residual");
+  if (bn && !(eps >= 0.f)) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: eps must be >= 0");
+  if ((bn && (!aligned16(gamma) || !aligned16(beta) || !aligned16(mean) || !aligned16(var))) ||
+      ((epi_flags & ICPP_CONV_EPI_RESIDUAL) && !aligned16(residual)))
+    return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: epilogue pointers must be 16-byte aligned");
   if (N <= 0 || H <= 0 || W <= 0 || C <= 0 || F <= 0 || KH <= 0 || KW <= 0 || stride <= 0 || pad < 0 || dilation <= 0)
     return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: bad geometry");
   if (split_k < 1) return fail(ICPP_E_ARG, "icpp_conv2d_nhwc: split_k=%d", split_k);
@@ -260,6 +287,11 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
   a.cH = H; a.cW = W; a.cC = C; a.cKH = KH; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH;
   a.cOW = OW;
   a.a_bytes_total = (uint32_t)xbytes;
+  a.act = act;
+  a.ce.flags = epi_flags;
+  a.ce.eps = eps;
+  a.ce.gamma = gamma; a.ce.beta = beta; a.ce.mean = mean; a.ce.var = var;
+  a.ce.residual = residual;
   hipStream_t s = (hipStream_t)stream;
   // every K tile inside one filter tap (and the tap set fits the 64-bit mask): per-tile-tap gather
   const LaunchFn launch = (C % t.block_k == 0 && KH * KW <= 64) ? in->launch : in->launch_gather;
@@ -272,7 +304,8 @@ int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
     a.ws = (float*)workspace;
     int rc = check_launch(launch(a, grid, s), t.name);
     if (rc) return rc;
-    return check_launch(launch_splitk_reduce(DT_F16, a.ws, Y, nullptr, a.M, F, F, a.splits, 1.f, ICPP_ACT_NONE, s), "splitk_reduce");
+    return check_launch(launch_splitk_reduce(DT_F16, a.ws, Y, nullptr, a.M, F, F, a.splits, 1.f, act, s, a.ce),
+                        "splitk_reduce");
   }
   return check_launch(launch(a, grid, s), t.name);
 }

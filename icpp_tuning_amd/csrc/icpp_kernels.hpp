@@ -58,6 +58,20 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 #define ICPP_INLINE __attribute__((always_inline))
 #define ICPP_BUF_DWORD3 0x00020000  // gfx9 raw buffer: 32-bit data format, no swizzle
 
+// Fused conv epilogue (conv2d family): y = act(BN(round_f16(conv)) + residual), where
+// BN(x) = (x - mean) * rsqrt(var + eps) * gamma + beta per output channel (inference
+// statistics). Flags select the parts; with no flags the plain bias/act epilogue runs.
+enum ConvEpiFlag { CEPI_BN = 1, CEPI_RESIDUAL = 2, CEPI_VAR_CLAMP = 4 };
+struct ConvEpiArgs {
+  int flags;
+  float eps;
+  const void* gamma;     // [N] f16
+  const void* beta;      // [N] f16
+  const void* mean;      // [N] f16
+  const void* var;       // [N] f16; negative values clamp to 0 with CEPI_VAR_CLAMP
+  const void* residual;  // [M, ldc] f16, the output's layout
+};
+
 // Kernel arguments (passed by value; everything the launcher resolved on the host).
 struct KArgs {
   const void* A;
@@ -80,6 +94,7 @@ struct KArgs {
   // implicit-GEMM conv geometry (A_IM2COL*); GEMM M = Nb*OH*OW, K = KH*KW*C
   int cH, cW, cC, cKH, cKW, cS, cP, cD, cOH, cOW;
   uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
+  ConvEpiArgs ce;          // fused conv epilogue (conv instances only)
 };
 
 template <int DT> struct DTraits;
@@ -209,6 +224,12 @@ __device__ __forceinline__ void dispatch_act(int act, F&& f) {
     default: f(std::integral_constant<int, ACT_NONE>{}); break;
   }
 }
+// Runtime activation of the fused conv epilogue: ReLU or none (the reference's variants)
+template <typename F>
+__device__ __forceinline__ void dispatch_relu(int act, F&& f) {
+  if (act == ACT_RELU) f(std::integral_constant<int, ACT_RELU>{});
+  else f(std::integral_constant<int, ACT_NONE>{});
+}
 // 16-byte buffer store; offsets >= the descriptor's range are dropped by the hardware
 __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, i32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
@@ -235,6 +256,11 @@ template <> struct Vec4Store<_Float16> {
     h4 h = *reinterpret_cast<const h4*>(p);
     return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
   }
+  static __device__ __forceinline__ f32x4 ld_lds(const char ICPP_LDS* p) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 h = *reinterpret_cast<const h4 ICPP_LDS*>(p);
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  }
 };
 template <> struct Vec4Store<__bf16> {
   static __device__ __forceinline__ void st(void* p, f32x4 v) {
@@ -252,12 +278,47 @@ template <> struct Vec4Store<__bf16> {
     b4 h = *reinterpret_cast<const b4*>(p);
     return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
   }
+  static __device__ __forceinline__ f32x4 ld_lds(const char ICPP_LDS* p) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    b4 h = *reinterpret_cast<const b4 ICPP_LDS*>(p);
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  }
 };
 template <> struct Vec4Store<float> {
   static __device__ __forceinline__ void st(void* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
   static __device__ __forceinline__ void st_lds(char ICPP_LDS* p, f32x4 v) { *reinterpret_cast<f32x4 ICPP_LDS*>(p) = v; }
   static __device__ __forceinline__ f32x4 ld(const void* p) { return *reinterpret_cast<const f32x4*>(p); }
+  static __device__ __forceinline__ f32x4 ld_lds(const char ICPP_LDS* p) { return *reinterpret_cast<const f32x4 ICPP_LDS*>(p); }
 };
+
+// Per-channel BN of columns n..n+3 for the fused conv epilogue, folded to
+// y = x * sc + sh with sc = rsqrt(var + eps) * gamma and sh = beta - mean * sc
+// (identity without CEPI_BN or past the last column). rsqrt is v_rsq_f32 (~1 ulp);
+// the fold differs from (x - mean) * rsqrt * gamma + beta by fp32 rounding only.
+template <typename PT>
+__device__ __forceinline__ void conv_bn4(const ConvEpiArgs& ce, int N, int n, f32x4& sc, f32x4& sh) {
+  sc = f32x4{1.f, 1.f, 1.f, 1.f};
+  sh = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (!(ce.flags & CEPI_BN) || n >= N) return;
+  const f32x4 g = Vec4Store<PT>::ld((const PT*)ce.gamma + n);
+  const f32x4 b = Vec4Store<PT>::ld((const PT*)ce.beta + n);
+  const f32x4 m = Vec4Store<PT>::ld((const PT*)ce.mean + n);
+  const f32x4 v = Vec4Store<PT>::ld((const PT*)ce.var + n);
+  const bool clamp = (ce.flags & CEPI_VAR_CLAMP) != 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    sc[e] = rsqrtf((clamp ? fmaxf(v[e], 0.f) : v[e]) + ce.eps) * g[e];
+    sh[e] = fmaf(-m[e], sc[e], b[e]);
+  }
+}
+// One group of 4 outputs: round the conv value to the output type (the reference
+// epilogues read it back from an f16 tile), BN, + residual, act.
+template <int ACT, typename OutT>
+__device__ __forceinline__ f32x4 conv_epi4(f32x4 v, f32x4 sc, f32x4 sh, f32x4 r) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = act_fn<ACT>(fmaf((float)(OutT)v[e], sc[e], sh[e]) + r[e]);
+  return v;
+}
 
 // ---------------------------------------------------------------------------
 // Tile geometry
@@ -696,18 +757,47 @@ gemm_kernel(KArgs p) {
     // (converted to OutT) into a private padded LDS region, then re-reads them as
     // 16-byte row chunks, so global stores cover whole contiguous row segments
     // instead of 8-byte pieces of 16 different rows.
-    auto store_staged = [&](auto&& value4) ICPP_INLINE {
+    // With a residual (RES), each band's residual rows are read the same way --
+    // 16-byte row chunks, the next band's loads in flight while the current one
+    // is computed -- written into the band's LDS region, and read back by each
+    // lane in the accumulator layout before it overwrites them with its outputs.
+    auto store_staged_impl = [&](auto RES, const OutT* res, auto&& value4) ICPP_INLINE {
+      constexpr bool HAS_RES = decltype(RES)::value;
       constexpr int OSZ = (int)sizeof(OutT);
       constexpr int ROWB_O = G::WTN * OSZ + 16;           // +16 B rotates rows across banks
       constexpr int REGION = MF * ROWB_O;
       constexpr int CPR_O = G::WTN * OSZ / 16;             // 16-byte chunks per output row
       constexpr int CHUNK_ELEMS = 16 / OSZ;
+      constexpr int NQ = (MF * CPR_O + 63) / 64;           // chunks per lane per band
       constexpr int PER_STAGE = G::STAGE_BYTES / REGION;  // wave regions per stage array
       static_assert(PER_STAGE * STAGES >= WM * WN, "epilogue staging must fit the LDS stages");
       static_assert((G::WTN * OSZ) % 16 == 0, "wave tile rows must be whole 16-byte chunks");
       // store descriptor over this tile's rows (launchers keep BM * ldc * OSZ < 2 GiB)
       const uint64_t rows = (uint64_t)(p.M > row0 ? min(p.M - row0, BM) : 0);
       const __amdgpu_buffer_rsrc_t rc = make_rsrc((OutT*)p.C + (size_t)row0 * p.ldc, (uint32_t)(rows * p.ldc * OSZ));
+      // chunk j of a band: its (row, 16-byte column) in the wave tile and byte offset in the tile's rows
+      auto chunk_off = [&](int tm, int q) ICPP_INLINE {
+        const int rr = q / CPR_O, cc = q % CPR_O;
+        const int r = wm * G::WTM + tm * MF + rr;  // row within the tile: rows >= M lie past the range
+        const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
+        return n < p.N ? (uint32_t)(r * p.ldc + n) * OSZ : ICPP_OOB_OFFSET;
+      };
+      i32x4 rnext[NQ];
+      __amdgpu_buffer_rsrc_t rr_src;
+      auto load_band = [&](int tm) ICPP_INLINE {
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+          const int q = j * 64 + lane;
+          // past the range (rows >= M, columns >= N): the hardware returns zeros
+          rnext[j] = ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O)
+                         ? __builtin_amdgcn_raw_buffer_load_b128(rr_src, chunk_off(tm, q), 0, 0)
+                         : i32x4{0, 0, 0, 0};
+        }
+      };
+      if constexpr (HAS_RES) {
+        rr_src = make_rsrc(res + (size_t)row0 * p.ldc, (uint32_t)(rows * p.ldc * OSZ));
+        load_band(0);
+      }
       const int w_arr = wave / PER_STAGE;
       char ICPP_LDS* arr = (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
                          : (w_arr == 2) ? (char ICPP_LDS*)lds2 : (char ICPP_LDS*)lds3;
@@ -715,33 +805,50 @@ gemm_kernel(KArgs p) {
       __syncthreads();  // every wave is done reading the pipeline stages
 #pragma unroll
       for (int tm = 0; tm < G::TM; ++tm) {
+        if constexpr (HAS_RES) {
+          i32x4 rcur[NQ];
+#pragma unroll
+          for (int j = 0; j < NQ; ++j) rcur[j] = rnext[j];
+          if (tm + 1 < G::TM) load_band(tm + 1);
+#pragma unroll
+          for (int j = 0; j < NQ; ++j) {
+            const int q = j * 64 + lane;
+            if ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O)
+              *(i32x4 ICPP_LDS*)(region + (q / CPR_O) * ROWB_O + (q % CPR_O) * 16) = rcur[j];
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
 #pragma unroll
         for (int tn = 0; tn < G::TN; ++tn)
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
-            const f32x4 v = value4(tm, tn, g);
             const int lcol = tn * MF + ((MF == 16) ? 4 * (lane >> 4) : (8 * g + 4 * (lane >> 5)));
-            Vec4Store<OutT>::st_lds(region + (lane % MF) * ROWB_O + lcol * OSZ, v);
+            char ICPP_LDS* at = region + (lane % MF) * ROWB_O + lcol * OSZ;
+            f32x4 r = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (HAS_RES) r = Vec4Store<OutT>::ld_lds(at);  // this lane's own elements
+            Vec4Store<OutT>::st_lds(at, value4(tm, tn, g, r));
           }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int q0 = 0; q0 < MF * CPR_O; q0 += 64) {
-          const int q = q0 + lane;
+        for (int j = 0; j < NQ; ++j) {
+          const int q = j * 64 + lane;
           if ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O) {
-            const int rr = q / CPR_O, cc = q % CPR_O;
-            const i32x4 v = *(const i32x4 ICPP_LDS*)(region + rr * ROWB_O + cc * 16);
-            const int r = wm * G::WTM + tm * MF + rr;  // row within the tile: rows >= M lie past the range
-            const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
-            const uint32_t off = (uint32_t)(r * p.ldc + n) * OSZ;
-            buf_store16(rc, n < p.N ? off : ICPP_OOB_OFFSET, v);
+            const i32x4 v = *(const i32x4 ICPP_LDS*)(region + (q / CPR_O) * ROWB_O + (q % CPR_O) * 16);
+            buf_store16(rc, chunk_off(tm, q), v);
           }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
+    };
+    auto store_staged = [&](auto&& value4) ICPP_INLINE {
+      store_staged_impl(std::false_type{}, nullptr,
+                        [&](int tm, int tn, int g, f32x4) ICPP_INLINE { return value4(tm, tn, g); });
     };
 
     if constexpr (EPI == EPI_STORE) {
@@ -757,6 +864,24 @@ gemm_kernel(KArgs p) {
               const int n = out_col(tn, g);
               if (m < p.M && n < p.N) Vec4Store<float>::st(ws + (size_t)m * p.N + n, get4(tm, tn, g));
             }
+        }
+      } else if (ALOAD != A_DENSE && p.ce.flags != 0) {
+        // fused conv epilogue (reference conv2d_bn / conv2d_bn_relu / conv_bn_add_relu)
+        if constexpr (ALOAD != A_DENSE) {
+          f32x4 sc[G::TN][NG], sh[G::TN][NG];
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) conv_bn4<BiasT>(p.ce, p.N, out_col(tn, g), sc[tn][g], sh[tn][g]);
+          auto run = [&](auto RES) ICPP_INLINE {
+            dispatch_relu(p.act, [&](auto ACT) ICPP_INLINE {
+              store_staged_impl(RES, (const OutT*)p.ce.residual, [&](int tm, int tn, int g, f32x4 r) ICPP_INLINE {
+                return conv_epi4<decltype(ACT)::value, OutT>(get4(tm, tn, g), sc[tn][g], sh[tn][g], r);
+              });
+            });
+          };
+          if (p.ce.flags & CEPI_RESIDUAL) run(std::true_type{});
+          else run(std::false_type{});
         }
       } else {
         const BiasT* bias = (const BiasT*)p.bias;
@@ -971,10 +1096,11 @@ gemm_kernel(KArgs p) {
 // ---------------------------------------------------------------------------
 // Split-K reduction + epilogue: C = act(alpha * sum_z ws[z] + bias)
 // ---------------------------------------------------------------------------
+// With ce.flags set (conv instances), the fused conv epilogue replaces bias/alpha.
 template <int DT>
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* __restrict__ ws, void* C, const void* bias, int M, int N, int ldc,
-                     int splits, float alpha, int act) {
+                     int splits, float alpha, int act, ConvEpiArgs ce) {
   typedef typename DTraits<DT>::OutT OutT;
   typedef typename DTraits<DT>::BiasT BiasT;
   const size_t groups = (size_t)M * (N / 4);
@@ -984,12 +1110,20 @@ splitk_reduce_kernel(const float* __restrict__ ws, void* C, const void* bias, in
     const int n = (int)(gi % (N / 4)) * 4;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     for (int z = 0; z < splits; ++z) s += Vec4Store<float>::ld(ws + ((size_t)z * M + m) * N + n);
-    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-    if (bias != nullptr) bv = Vec4Store<BiasT>::ld((const BiasT*)bias + n);
-    dispatch_act(act, [&](auto ACT) {
+    if (ce.flags != 0) {
+      f32x4 sc, sh;
+      conv_bn4<BiasT>(ce, N, n, sc, sh);
+      f32x4 r = {0.f, 0.f, 0.f, 0.f};
+      if (ce.flags & CEPI_RESIDUAL) r = Vec4Store<OutT>::ld((const OutT*)ce.residual + (size_t)m * ldc + n);
+      dispatch_relu(act, [&](auto ACT) { s = conv_epi4<decltype(ACT)::value, OutT>(s, sc, sh, r); });
+    } else {
+      f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+      if (bias != nullptr) bv = Vec4Store<BiasT>::ld((const BiasT*)bias + n);
+      dispatch_act(act, [&](auto ACT) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[e] = act_fn<decltype(ACT)::value>(s[e] * alpha + bv[e]);
-    });
+        for (int e = 0; e < 4; ++e) s[e] = act_fn<decltype(ACT)::value>(s[e] * alpha + bv[e]);
+      });
+    }
     Vec4Store<OutT>::st((OutT*)C + (size_t)m * ldc + n, s);
   }
 }

@@ -68,6 +68,20 @@ def config4(N=32, H=56, W=56, C=64, F=64, KH=3, KW=3, device="cpu"):
     return {"X": X.to(device), "W": Wt.to(device)}
 
 
+def bn_params(F: int, seed: int = 4100, device="cpu"):
+    """Inference BatchNorm parameters [F] f16 as the reference's fused-conv checks draw
+    them (conv_bn_add_relu.py:195-198): gamma, beta, mean ~ N(0, 1), var ~ U(0.5, 1.5)."""
+    g = torch.Generator().manual_seed(seed)
+    out = {k: torch.randn(F, generator=g).to(torch.float16) for k in ("gamma", "beta", "mean")}
+    out["var"] = (torch.rand(F, generator=g) + 0.5).to(torch.float16)
+    return {k: v.to(device) for k, v in out.items()}
+
+
+def residual(shape, seed: int = 4200, device="cpu"):
+    """Residual input [N, OH, OW, F] f16 ~ N(0, 1) (conv_bn_add_relu.py:194)."""
+    return normal(shape, 1.0, seed).to(torch.float16).to(device)
+
+
 def config5(M=256, N=4096, K=4096, device="cpu"):
     a = normal((M, K), 1.0, 5000 + 0)
     b = normal((K, N), 1.0 / math.sqrt(K), 5000 + 1)

@@ -1,0 +1,21 @@
+"""Conv2d + BatchNorm (inference) + ReLU (reference kernel/tilelang/conv/
+conv2d_bn_relu.py): ``get_configs``, ``build_conv2d_bn_relu_kernel`` (:272-279,
+``kernel(X, W, gamma, beta, mean, var, Y)``, eps 1e-5), ``estimate_total_flops``
+(:282-290) and ``DESCRIPTOR`` (:462-477)."""
+
+from .conv2d import get_configs  # noqa: F401
+from .conv2d_fused import DESCRIPTORS, build_fused_conv2d_kernel
+from .conv2d_fused import estimate_total_flops as _flops
+
+DESCRIPTOR = DESCRIPTORS["conv2d_bn_relu"]
+
+
+def build_conv2d_bn_relu_kernel(N, C, H, W, F_out, KH, KW, S=1, P=1, D=1, config=None):
+    return build_fused_conv2d_kernel("conv2d_bn_relu", N, C, H, W, F_out, KH, KW, S, P, D, config)
+
+
+def estimate_total_flops(N, OH, OW, F_out, C, KH, KW):
+    return _flops("conv2d_bn_relu", N, OH, OW, F_out, C, KH, KW)
+
+
+__all__ = ["DESCRIPTOR", "build_conv2d_bn_relu_kernel", "estimate_total_flops", "get_configs"]

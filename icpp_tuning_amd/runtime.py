@@ -12,7 +12,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import ACT, FAMILY, lib
+from ._lib import ACT, CONV_EPI, FAMILY, lib
 
 TORCH_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
 OUT_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.bfloat16}
@@ -96,8 +96,12 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
 
 
 def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, stride: int = 1, pad: int = 1,
-                dilation: int = 1, split_k: int = 1, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y[N,OH,OW,F] = conv2d(x[N,H,W,C], w[KH,KW,C,F]) through icpp_conv2d_nhwc (f16)."""
+                dilation: int = 1, split_k: int = 1, workspace: Optional[torch.Tensor] = None, *,
+                act: str = "none", bn: Optional[tuple] = None, eps: float = 1e-5, var_clamp: bool = False,
+                residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y[N,OH,OW,F] = conv2d(x[N,H,W,C], w[KH,KW,C,F]) (f16) through icpp_conv2d_nhwc, or with
+    a fused epilogue y = act(BN(conv) + residual) through icpp_conv2d_nhwc_fused:
+    bn = (gamma, beta, mean, var), each [F] f16; residual [N,OH,OW,F] f16; act "none" / "relu"."""
     N, H, W, C = x.shape
     KH, KW, C2, F = w.shape
     if C2 != C:
@@ -113,8 +117,24 @@ def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, st
         workspace = alloc_workspace(need, x.device)
     pws = workspace.data_ptr() if (need and workspace is not None) else None
     wsb = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
-    lib().call("icpp_conv2d_nhwc", inst, px, pw, py, N, H, W, C, F, KH, KW, stride, pad, dilation,
-               split_k, pws, wsb, _stream())
+    if act == "none" and bn is None and residual is None:
+        lib().call("icpp_conv2d_nhwc", inst, px, pw, py, N, H, W, C, F, KH, KW, stride, pad, dilation,
+                   split_k, pws, wsb, _stream())
+        return y
+    flags = 0
+    pbn = [None] * 4
+    if bn is not None:
+        if len(bn) != 4:
+            raise ValueError("bn must be (gamma, beta, mean, var)")
+        pbn = [_check(t, nm, h, (F,)) for t, nm in zip(bn, ("gamma", "beta", "mean", "var"))]
+        flags |= CONV_EPI["bn"] | (CONV_EPI["var_clamp"] if var_clamp else 0)
+    elif var_clamp:
+        raise ValueError("var_clamp needs bn")
+    pres = _check(residual, "residual", h, (N, OH, OW, F))
+    if residual is not None:
+        flags |= CONV_EPI["residual"]
+    lib().call("icpp_conv2d_nhwc_fused", inst, px, pw, py, pres, *pbn, float(eps), flags, ACT[act],
+               N, H, W, C, F, KH, KW, stride, pad, dilation, split_k, pws, wsb, _stream())
     return y
 
 

@@ -103,12 +103,40 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
  * Y[N,OH,OW,F] = conv2d(X[N,H,W,C], W[KH,KW,C,F]), f16, fp32 accumulate.
  * Replaces make_conv2d_kernel / build_conv2d_kernel (conv2d.py:208-290):
  * destination-passing like the reference's kernel(X, W, Y).
- * Requires C % 8 == 0, F % 8 == 0, (KH*KW*C) % (block_k * split_k) == 0.
+ * Requires C % 8 == 0, F % 8 == 0, (KH*KW*C) % block_k == 0 and
+ * split_k <= KH*KW*C / block_k; split_k > 1 needs split_k*M*F*4 workspace bytes.
  */
 int icpp_conv2d_nhwc(int inst, const void* X, const void* Wt, void* Y,
                      int N, int H, int W, int C, int F, int KH, int KW,
                      int stride, int pad, int dilation, int split_k,
                      void* workspace, size_t ws_bytes, void* stream);
+
+/* Fused conv epilogue parts (icpp_conv2d_nhwc_fused epi_flags). */
+enum icpp_conv_epi {
+  ICPP_CONV_EPI_BN = 1,        /* inference BatchNorm per output channel */
+  ICPP_CONV_EPI_RESIDUAL = 2,  /* + residual[N,OH,OW,F] */
+  ICPP_CONV_EPI_VAR_CLAMP = 4  /* clamp var at 0 before rsqrt (with BN) */
+};
+
+/*
+ * Y = act(BN(conv2d(X, W)) + residual): the conv of icpp_conv2d_nhwc with a
+ * fused epilogue, act in {ICPP_ACT_NONE, ICPP_ACT_RELU}. With BN the conv value
+ * is rounded to f16 first, then BN(x) = (x - mean) * rsqrt(var + eps) * gamma
+ * + beta in fp32 (gamma, beta, mean, var: [F] f16); the residual (f16, Y's
+ * layout) is added in fp32 and the sum rounded to f16 once. Replaces the
+ * reference's fused conv kernels:
+ *   conv2d_relu.py:63-143      flags 0,                      ICPP_ACT_RELU
+ *   conv2d_bn.py:67-156        BN (eps 1e-3 there),          ICPP_ACT_NONE
+ *   conv2d_bn_relu.py:185-269  BN (eps 1e-5),                ICPP_ACT_RELU
+ *   conv_bn_add_relu.py:73-166 BN|RESIDUAL|VAR_CLAMP (1e-5), ICPP_ACT_RELU
+ * Same shape rules as icpp_conv2d_nhwc; epilogue pointers 16-byte aligned.
+ */
+int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, const void* residual,
+                           const void* gamma, const void* beta, const void* mean, const void* var,
+                           float eps, int epi_flags, int act,
+                           int N, int H, int W, int C, int F, int KH, int KW,
+                           int stride, int pad, int dilation, int split_k,
+                           void* workspace, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

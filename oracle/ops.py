@@ -65,6 +65,27 @@ def conv2d_nhwc_ref(X, Wt, stride: int = 1, padding: int = 1, dilation: int = 1)
     return y.permute(0, 2, 3, 1).contiguous()
 
 
+def conv2d_bn_act_ref(X, Wt, stride: int = 1, padding: int = 1, dilation: int = 1, bn=None, eps: float = 1e-5,
+                      var_clamp: bool = False, residual=None, act: str = "none") -> torch.Tensor:
+    """Fused conv epilogues in fp32, following the reference's torch programs:
+      conv2d_relu.py:29-60       relu(conv)
+      conv2d_bn.py:29-62         BN(conv), eps 1e-3 there
+      conv2d_bn_relu.py:123-160  relu(BN(conv)), eps 1e-5
+      conv_bn_add_relu.py:28-68  relu(BN(conv) + residual), var clamped at 0, eps 1e-5
+    Each runs F.conv2d on f16 tensors, so its conv output is f16 before the
+    epilogue's fp32 arithmetic: the conv is rounded to f16 here too.  BN(x) =
+    (x - mean) * rsqrt(var + eps) * gamma + beta per output channel."""
+    y = conv2d_nhwc_ref(X, Wt, stride, padding, dilation).to(torch.float16).float()
+    if bn is not None:
+        gamma, beta, mean, var = (t.float().cpu() for t in bn)
+        if var_clamp:
+            var = torch.clamp(var, min=0.0)
+        y = (y - mean) * torch.rsqrt(var + eps) * gamma + beta
+    if residual is not None:
+        y = y + residual.float().cpu()
+    return apply_act(y, act)
+
+
 def conv_out_hw(H, W, KH, KW, S, P, D=1):
     """reference conv2d.py:65-68"""
     return (H + 2 * P - D * (KH - 1) - 1) // S + 1, (W + 2 * P - D * (KW - 1) - 1) // S + 1

@@ -84,3 +84,26 @@ def test_validation_errors_before_launch(L):
     assert f(row, 0, 16, 16, None, 16, 16, 16, 64, 2048, 64, 1e-5, None, 0, None) == -2  # N > block_n
     c = L._dll.icpp_conv2d_nhwc
     assert c(0, 16, 16, 16, 1, 8, 8, 3, 64, 3, 3, 1, 1, 1, 1, None, 0, None) == -2  # C % 8
+
+
+def test_fused_conv_validation_errors_before_launch(L):
+    """icpp_conv2d_nhwc_fused rejects inconsistent epilogue arguments before any
+    device work (pointers are never dereferenced on these paths)."""
+    f = L._dll.icpp_conv2d_nhwc_fused
+    geo = (2, 8, 8, 64, 64, 3, 3, 1, 1, 1, 1, None, 0, None)   # N H W C F KH KW s p d split ws wsb stream
+
+    def call(res=None, g=None, b=None, m=None, v=None, eps=1e-5, flags=0, act=0, X=16, Y=16):
+        return f(0, X, 16, Y, res, g, b, m, v, ctypes.c_float(eps), flags, act, *geo)
+
+    BN, RES, CLAMP = _lib.CONV_EPI["bn"], _lib.CONV_EPI["residual"], _lib.CONV_EPI["var_clamp"]
+    assert call(flags=8) == -4                                  # unknown flag
+    assert call(act=_lib.ACT["silu"]) == -4                     # only none / relu
+    assert call(flags=BN) == -4                                 # BN without its parameters
+    assert call(flags=BN, g=16, b=16, m=16) == -4               # ... var missing
+    assert call(flags=CLAMP) == -4                              # clamp without BN
+    assert call(flags=RES) == -4                                # residual flag, no residual
+    assert call(flags=BN, g=16, b=16, m=16, v=16, eps=-1.0) == -4
+    assert call(flags=BN, g=24, b=16, m=16, v=16) == -4         # misaligned gamma
+    assert call(flags=RES, res=40) == -4                        # misaligned residual
+    assert call(X=None) == -4
+    assert "icpp_conv2d_nhwc" in L.last_error()

@@ -13,7 +13,7 @@ import torch
 
 from icpp_tuning_amd import inputs as I
 from icpp_tuning_amd.autotuner import get_gpu_spec
-from icpp_tuning_amd.autotuner.perfdb import AdaptiveTuner, PerformanceDB, build_db
+from icpp_tuning_amd.autotuner.perfdb import AdaptiveTuner, PerformanceDB, build_db, op_key
 from icpp_tuning_amd.kernels import gemm_bias_act as gba_mod
 from oracle import ops as O
 
@@ -27,7 +27,7 @@ def test_db_from_device_measurements(gpu, tmp_path):
     db = build_db(desc, shapes, top_k=3, budget_ms=10.0, reps=5)
     db.save(tmp_path / "db.json")
     db = PerformanceDB.load(tmp_path / "db.json")
-    assert db.hw == get_gpu_spec().name and db.op == desc.name
+    assert db.hw == get_gpu_spec().name and db.op == op_key(desc)
     tuner = AdaptiveTuner(desc, db)
     for s in shapes:
         recs = [r for r in db.records if r.shape == s]

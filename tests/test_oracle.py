@@ -168,3 +168,92 @@ def test_seeded_inputs_are_deterministic():
     for k in a:
         assert torch.equal(a[k], b[k])
     assert abs(I.config2(64, 64, 4096)["B"].float().std().item() - 1 / 64) < 2e-3
+
+
+# ---- fused conv epilogues (conv2d_bn_act_ref) ----
+
+def _conv_case(seed=21, N=2, H=5, W=6, C=8, Fo=8):
+    d = I.config4(N, H, W, C, Fo)
+    bn = I.bn_params(Fo, seed=seed)
+    return d["X"], d["W"], bn
+
+
+def test_conv_bn_matches_torch_batch_norm_eval():
+    """BN against torch's own inference batch_norm (running stats, affine) on the
+    f16-rounded conv output: pins the (x - mean) / sqrt(var + eps) * gamma + beta
+    terms and the eps placement."""
+    X, Wt, bn = _conv_case()
+    for eps in (1e-3, 1e-5):
+        y16 = O.conv2d_nhwc_ref(X, Wt).to(torch.float16).float().permute(0, 3, 1, 2)
+        want = F.batch_norm(y16, bn["mean"].float(), bn["var"].float(), bn["gamma"].float(), bn["beta"].float(),
+                            training=False, eps=eps).permute(0, 2, 3, 1)
+        got = O.conv2d_bn_act_ref(X, Wt, bn=tuple(bn[k] for k in ("gamma", "beta", "mean", "var")), eps=eps)
+        torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-6)
+        relu = O.conv2d_bn_act_ref(X, Wt, bn=tuple(bn[k] for k in ("gamma", "beta", "mean", "var")), eps=eps,
+                                   act="relu")
+        torch.testing.assert_close(relu, torch.clamp_min(want, 0.0), rtol=1e-6, atol=1e-6)
+
+
+def test_conv_bn_add_relu_matches_fp64_loops():
+    """Every term of relu(BN(round16(conv)) + residual) from fp64 per-element loops."""
+    X, Wt, bn = _conv_case(seed=22, N=1, H=4, W=5, C=8, Fo=8)
+    R = I.residual((1, 4, 5, 8), seed=23)
+    y = O.conv2d_nhwc_ref(X, Wt).double().numpy()
+    g, b, m, v = (_np64(bn[k]) for k in ("gamma", "beta", "mean", "var"))
+    r = _np64(R)
+    want = np.zeros_like(y)
+    for idx in np.ndindex(*y.shape):
+        f = idx[-1]
+        x16 = float(np.float16(y[idx]))
+        z = (x16 - m[f]) / math.sqrt(max(v[f], 0.0) + 1e-5) * g[f] + b[f] + r[idx]
+        want[idx] = max(z, 0.0)
+    got = O.conv2d_bn_act_ref(X, Wt, bn=tuple(bn[k] for k in ("gamma", "beta", "mean", "var")), eps=1e-5,
+                              var_clamp=True, residual=R, act="relu")
+    np.testing.assert_allclose(got.double().numpy(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_conv_bn_identity_and_residual_special_cases():
+    X, Wt, _ = _conv_case(seed=24)
+    Fo = Wt.shape[-1]
+    eps = 1e-5
+    one = torch.ones(Fo, dtype=torch.float32)
+    # gamma 1, beta 0, mean 0, var 1 - eps: rsqrt(1) = 1, the output is the f16 conv exactly
+    ident = (one, 0 * one, 0 * one, one - eps)
+    y16 = O.conv2d_nhwc_ref(X, Wt).to(torch.float16).float()
+    assert torch.equal(O.conv2d_bn_act_ref(X, Wt, bn=ident, eps=eps), y16)
+    # residual of -conv cancels: relu(0) = 0 everywhere
+    R = (-y16).to(torch.float16)
+    assert torch.equal(O.conv2d_bn_act_ref(X, Wt, bn=ident, eps=eps, residual=R, act="relu"), torch.zeros_like(y16))
+    # relu only: relu of the (rounded) conv
+    assert torch.equal(O.conv2d_bn_act_ref(X, Wt, act="relu"), torch.clamp_min(y16, 0.0))
+
+
+def test_conv_bn_var_clamp():
+    """Negative variances: clamped to 0 (conv_bn_add_relu.py:158) or left to give NaN."""
+    X, Wt, bn = _conv_case(seed=25)
+    var = bn["var"].clone()
+    var[::2] = -0.75
+    p = (bn["gamma"], bn["beta"], bn["mean"], var)
+    clamped = O.conv2d_bn_act_ref(X, Wt, bn=p, eps=1e-5, var_clamp=True)
+    zero_var = O.conv2d_bn_act_ref(X, Wt, bn=(bn["gamma"], bn["beta"], bn["mean"], torch.where(var < 0, 0 * var, var)),
+                                   eps=1e-5)
+    assert torch.equal(clamped, zero_var) and torch.isfinite(clamped).all()
+    raw = O.conv2d_bn_act_ref(X, Wt, bn=p, eps=1e-5)
+    assert torch.isnan(raw[..., ::2]).all() and torch.isfinite(raw[..., 1::2]).all()
+
+
+def test_conv_epilogue_rounds_conv_to_f16_first():
+    """A conv value of 1 + 2^-11 (exact in fp32, a tie in f16 that rounds to 1.0)
+    then BN with mean 1 and a scale of 2048: the reference's f16 tile gives 0, an
+    unrounded value would give 1."""
+    X = torch.zeros(1, 1, 1, 8, dtype=torch.float16)
+    X[..., 0] = 1.0
+    X[..., 1] = 2.0 ** -11
+    Wt = torch.zeros(1, 1, 8, 8, dtype=torch.float16)
+    Wt[0, 0, 0, :] = 1.0
+    Wt[0, 0, 1, :] = 1.0
+    assert float(O.conv2d_nhwc_ref(X, Wt, 1, 0)[0, 0, 0, 0]) == 1.0 + 2.0 ** -11
+    eps = 1e-5
+    ones = torch.ones(8)
+    y = O.conv2d_bn_act_ref(X, Wt, 1, 0, bn=(2048 * ones, 0 * ones, ones, ones - eps), eps=eps)
+    assert torch.equal(y, torch.zeros_like(y))
