@@ -172,6 +172,51 @@ def bench_ops(quick: bool, only: str = ""):
             record(variant, d, shape, d.flops(**shape),
                    2 * (Nb * H * W * C + 9 * C * F + Nb * H * W * F + 4 * F + (Nb * H * W * F if d.residual else 0)),
                    "f16")
+    # standalone row ops (reference kernel/triton/softmax.py / layernorm.py benchmarks: M = 4096, GB/s of
+    # 2 M N elements for softmax and the LayerNorm forward, 3 M N for the LayerNorm backward)
+    from icpp_tuning_amd import runtime as RT
+
+    def record_rows(op, shape, dtype, make, nbytes):
+        if only and not op.startswith(only):
+            return
+        copies = max(1, min(16, -(-(600 << 20) // max(1, nbytes))))
+        runs = [make(i) for i in range(copies)]
+        ms = benchmark_ms(runs, warmup=copies, reps=max(20, 2 * copies))
+        del runs
+        gbps = nbytes / ms / 1e6
+        rows.append({"op": op, "shape": shape, "dtype": dtype, "input_copies": copies, "ms": round(ms, 5),
+                     "gbps": round(gbps, 1), "pct_hbm": round(100 * gbps / HBM_GBPS, 2), "bound": "hbm"})
+        print(f"[bench] {op} {shape}: {ms*1e3:.1f} us, {gbps:.0f} GB/s ({100 * gbps / HBM_GBPS:.1f}% of HBM)",
+              file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+
+    def _softmax(M, N, dt):
+        def make(i):
+            g = torch.Generator(device="cuda").manual_seed(i)
+            x = torch.randn(M, N, generator=g, device="cuda", dtype=dt)
+            y = torch.empty_like(x)
+            return lambda: RT.softmax(x, out=y)
+        return make
+
+    def _ln(M, N, backward):
+        def make(i):
+            g = torch.Generator(device="cuda").manual_seed(i)
+            x = (-2.3 + 0.5 * torch.randn(M, N, generator=g, device="cuda")).half()
+            w = torch.rand(N, generator=g, device="cuda").half()
+            b = torch.rand(N, generator=g, device="cuda").half()
+            y, mean, rstd = RT.layernorm_fwd(x, w, b)
+            if not backward:
+                return lambda: RT.layernorm_fwd(x, w, b, out=y)
+            dy = (0.1 * torch.randn(M, N, generator=g, device="cuda")).half()
+            return lambda: RT.layernorm_bwd(dy, x, w, mean, rstd)
+        return make
+
+    for N in ([4096] if quick else [1024, 4096, 12288]):
+        record_rows("softmax", dict(M=4096, N=N), "f32", _softmax(4096, N, torch.float32), 2 * 4096 * N * 4)
+    for N in ([4096] if quick else [1024, 4096, 8192, 15872]):
+        record_rows("layernorm_fwd", dict(M=4096, N=N), "f16", _ln(4096, N, False), 2 * 4096 * N * 2)
+        record_rows("layernorm_bwd", dict(M=4096, N=N), "f16", _ln(4096, N, True), 3 * 4096 * N * 2)
+
     f8_shapes = [(16, 4096, 4096), (4096, 4096, 4096)] if quick else [
         (m, n, k) for m in (16, 256, 4096) for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008))]
     for (M, N, K) in f8_shapes:

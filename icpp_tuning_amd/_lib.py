@@ -20,7 +20,7 @@ RESOURCES_PATH = PKG / "libicpp_hip.resources.json"
 ABI_VERSION = 1
 FAMILY = {"gemm": 0, "gemm_ln_stats": 1, "gemm_ln_row": 2, "conv2d": 3}
 FAMILY_NAME = {v: k for k, v in FAMILY.items()}
-DTYPE = {"f16": 0, "bf16": 1, "fp8": 2}
+DTYPE = {"f16": 0, "bf16": 1, "fp8": 2, "f32": 3}
 DTYPE_NAME = {v: k for k, v in DTYPE.items()}
 ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu": 2, "silu": 3}
 
@@ -28,6 +28,7 @@ ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu": 2, "silu": 3}
 EXPORTED_SYMBOLS = (
     "icpp_abi_version", "icpp_last_error", "icpp_num_instances", "icpp_instance_info",
     "icpp_workspace_bytes", "icpp_gemm", "icpp_gemm_bias_layernorm", "icpp_conv2d_nhwc", "icpp_conv2d_nhwc_fused",
+    "icpp_layernorm_fwd", "icpp_layernorm_bwd_workspace_bytes", "icpp_layernorm_bwd", "icpp_softmax",
 )
 CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
@@ -64,6 +65,10 @@ _SIGNATURES = {
     "icpp_conv2d_nhwc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "icpp_conv2d_nhwc_fused": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i,
                                     _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "icpp_layernorm_fwd": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
+    "icpp_layernorm_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "icpp_layernorm_bwd": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "icpp_softmax": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
 }
 
 
@@ -100,6 +105,9 @@ class Lib:
 
     def workspace_bytes(self, family: int, inst: int, M: int, N: int, K: int, split_k: int) -> int:
         return int(self._dll.icpp_workspace_bytes(family, inst, M, N, K, split_k))
+
+    def layernorm_bwd_workspace_bytes(self, dtype: int, M: int, N: int, ld: int) -> int:
+        return int(self._dll.icpp_layernorm_bwd_workspace_bytes(dtype, M, N, ld))
 
     # ---- instance table --------------------------------------------------
     def instances(self, family: int) -> List[dict]:

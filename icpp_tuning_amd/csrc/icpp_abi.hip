@@ -105,6 +105,9 @@ int register_instance(const Instance& inst) {
   return (int)table(inst.tile.family).size();
 }
 
+// The row-op translation unit (icpp_rowops.hip) reports through the same buffer.
+int set_last_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
 }  // namespace icpp
 
 using namespace icpp;

@@ -1,0 +1,545 @@
+// Row-wise kernels for gfx950: LayerNorm forward / backward and softmax over the
+// last dimension of a [M, N] row-major tensor (row stride ld >= N).
+//
+// Reference: kernel/triton/layernorm.py (_layer_norm_fwd_fused :48-91,
+// _layer_norm_bwd_dx_fused :128-181, _layer_norm_bwd_dwdb :184-207,
+// LayerNorm.forward/backward :219-275) and kernel/triton/softmax.py
+// (softmax_kernel :32-55, softmax :73-102).
+//
+// Layout: each row is split into chunks of VEC elements (16 bytes: 8 x f16/bf16,
+// 4 x f32; VEC = 1 when N, the strides or the pointers are not 16-byte multiples).
+// TPR threads share a row (a power of two, 64..1024); thread t owns chunks
+// t, t + TPR, ... (CPT of them), so each wave instruction reads a contiguous
+// 1 KiB of the row. A row is loaded into registers once: every statistic and
+// the output come from registers (HBM traffic = the algorithmic bytes).
+// Reductions: xor-shuffles within the wave, then LDS across the row's waves.
+//
+// LayerNorm backward writes dx per row and accumulates dw / db in fp32
+// registers: a persistent grid of G <= 256 workgroups walks the rows, each
+// thread always owning the same columns; the row slots of a workgroup are
+// folded together through LDS and one fp32 partial row per workgroup goes to
+// the workspace, which a column-sum kernel reduces in a fixed order
+// (deterministic; no locks or atomics, unlike the reference's
+// lock-protected fp16 partial buffers).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "icpp_hip.h"
+
+namespace icpp_rows {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int MAX_WAVES = 16;   // 1024 threads
+constexpr int BWD_BLOCK = 1024;
+constexpr int BWD_MAX_GROUPS = 256;
+
+template <typename T> __device__ __forceinline__ float to_f(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+
+// VEC elements of T at p (16-byte aligned when VEC > 1) <-> floats
+template <typename T, int VEC>
+__device__ __forceinline__ void load_chunk(const T* p, float* out) {
+  if constexpr (VEC == 1) {
+    out[0] = to_f(*p);
+  } else {
+    const i32x4 raw = *reinterpret_cast<const i32x4*>(p);
+    T e[VEC];
+    __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) out[i] = to_f(e[i]);
+  }
+}
+template <typename T, int VEC>
+__device__ __forceinline__ void store_chunk(T* p, const float* in) {
+  if constexpr (VEC == 1) {
+    *p = from_f<T>(in[0]);
+  } else {
+    T e[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) e[i] = from_f<T>(in[i]);
+    i32x4 raw;
+    __builtin_memcpy(&raw, e, 16);
+    *reinterpret_cast<i32x4*>(p) = raw;
+  }
+}
+
+struct Sum { __device__ float operator()(float a, float b) const { return a + b; } };
+struct Max { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Reduce v over the TPR threads of each row. Every thread of the block calls it
+// the same number of times (one __syncthreads each); slot alternates between two
+// LDS buffers so a reduction never overwrites values another wave may still read.
+template <typename Op>
+__device__ __forceinline__ float row_reduce(float v, Op op, int tpr, float (*red)[MAX_WAVES], int& slot) {
+  v = wave_reduce(v, op);
+  if (tpr <= 64) return v;
+  const int wave = threadIdx.x >> 6;
+  const int wpr = tpr >> 6;                // waves per row
+  const int first = (wave / wpr) * wpr;    // first wave of this row
+  if ((threadIdx.x & 63) == 0) red[slot][wave] = v;
+  __syncthreads();
+  float r = red[slot][first];
+  for (int w = 1; w < wpr; ++w) r = op(r, red[slot][first + w]);
+  slot ^= 1;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm forward: y = (x - mean) * rstd * w + b, mean / rstd (fp32) per row
+// (reference _layer_norm_fwd_fused: centred two-pass variance, rstd = 1/sqrt(var+eps)).
+// ---------------------------------------------------------------------------
+template <typename T, int VEC, int CPT>
+__global__ void __launch_bounds__(1024)
+layernorm_fwd_kernel(const T* __restrict__ X, const T* __restrict__ W, const T* __restrict__ B, T* __restrict__ Y,
+                     float* __restrict__ mean_out, float* __restrict__ rstd_out, int M, int N, int ldx, int ldy,
+                     float eps, int tpr) {
+  __shared__ float red[2][MAX_WAVES];
+  int slot = 0;
+  const int rpb = blockDim.x / tpr;
+  const int row = blockIdx.x * rpb + threadIdx.x / tpr;
+  const int t = threadIdx.x % tpr;
+  const bool live = row < M;
+  const int nch = (N + VEC - 1) / VEC;
+  float x[CPT][VEC];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (live && c < nch) load_chunk<T, VEC>(X + (size_t)row * ldx + (size_t)c * VEC, x[i]);
+    else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) s += x[i][e];
+  }
+  const float mean = row_reduce(s, Sum{}, tpr, red, slot) / (float)N;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (c < nch) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = x[i][e] - mean;
+        q += d * d;
+      }
+    }
+  }
+  const float var = row_reduce(q, Sum{}, tpr, red, slot) / (float)N;
+  const float rstd = 1.f / sqrtf(var + eps);
+  if (live && t == 0) {
+    if (mean_out) mean_out[row] = mean;
+    if (rstd_out) rstd_out[row] = rstd;
+  }
+  if (!live) return;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (c < nch) {
+      float w[VEC], b[VEC], y[VEC];
+      load_chunk<T, VEC>(W + (size_t)c * VEC, w);
+      load_chunk<T, VEC>(B + (size_t)c * VEC, b);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) y[e] = (x[i][e] - mean) * rstd * w[e] + b[e];
+      store_chunk<T, VEC>(Y + (size_t)row * ldy + (size_t)c * VEC, y);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax over each row: exp(x - max) / sum (reference softmax_kernel; the
+// arithmetic is fp32 whatever the storage type).
+// ---------------------------------------------------------------------------
+template <typename T, int VEC, int CPT>
+__global__ void __launch_bounds__(1024)
+softmax_kernel(const T* __restrict__ X, T* __restrict__ Y, int M, int N, int ldx, int ldy, int tpr) {
+  __shared__ float red[2][MAX_WAVES];
+  int slot = 0;
+  const int rpb = blockDim.x / tpr;
+  const int row = blockIdx.x * rpb + threadIdx.x / tpr;
+  const int t = threadIdx.x % tpr;
+  const bool live = row < M;
+  const int nch = (N + VEC - 1) / VEC;
+  float x[CPT][VEC];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (live && c < nch) {
+      load_chunk<T, VEC>(X + (size_t)row * ldx + (size_t)c * VEC, x[i]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) m = fmaxf(m, x[i][e]);
+    }
+  }
+  m = row_reduce(m, Max{}, tpr, red, slot);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (live && c < nch) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        x[i][e] = expf(x[i][e] - m);
+        s += x[i][e];
+      }
+    }
+  }
+  s = row_reduce(s, Sum{}, tpr, red, slot);
+  if (!live) return;
+  const float inv = 1.f / s;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (c < nch) {
+      float y[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) y[e] = x[i][e] * inv;
+      store_chunk<T, VEC>(Y + (size_t)row * ldy + (size_t)c * VEC, y);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm backward, pass 1 (reference _layer_norm_bwd_dx_fused :128-181):
+//   xhat = (x - mean) * rstd, wdy = w * dy
+//   c1 = sum(xhat * wdy) / N, c2 = sum(wdy) / N
+//   dx = (wdy - (xhat * c1 + c2)) * rstd
+// plus dw = sum_rows dy * xhat and db = sum_rows dy, accumulated per thread in
+// fp32 and written as one partial row per workgroup: part[g][0..N) = dw,
+// part[g][N..2N) = db.
+// ---------------------------------------------------------------------------
+template <typename T, int VEC, int CPT>
+__global__ void __launch_bounds__(BWD_BLOCK)
+layernorm_bwd_kernel(const T* __restrict__ DY, const T* __restrict__ X, const T* __restrict__ W,
+                     const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ DX,
+                     float* __restrict__ part, int M, int N, int ld, int tpr) {
+  __shared__ float red[2][MAX_WAVES];
+  __shared__ f32x4 fold[BWD_BLOCK];  // row-slot folding, one 16-byte value per thread
+  int slot = 0;
+  const int rpb = blockDim.x / tpr;
+  const int rs = threadIdx.x / tpr;  // row slot within the workgroup
+  const int t = threadIdx.x % tpr;
+  const int nch = (N + VEC - 1) / VEC;
+  const float inv_n = 1.f / (float)N;
+  float w[CPT][VEC], dw[CPT][VEC], db[CPT][VEC];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    if (c < nch) load_chunk<T, VEC>(W + (size_t)c * VEC, w[i]);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      if (c >= nch) w[i][e] = 0.f;
+      dw[i][e] = 0.f;
+      db[i][e] = 0.f;
+    }
+  }
+  // rows rs + rpb * (blockIdx.x + k * gridDim.x): every thread runs the same trip count
+  const int stride = rpb * gridDim.x;
+  for (int base = blockIdx.x * rpb; base < M; base += stride) {
+    const int row = base + rs;
+    const bool live = row < M;
+    const float mean = live ? mean_in[row] : 0.f;
+    const float rstd = live ? rstd_in[row] : 0.f;
+    float xh[CPT][VEC], wdy[CPT][VEC], dyv[CPT][VEC];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = t + i * tpr;
+      float xv[VEC];
+      if (live && c < nch) {
+        load_chunk<T, VEC>(X + (size_t)row * ld + (size_t)c * VEC, xv);
+        load_chunk<T, VEC>(DY + (size_t)row * ld + (size_t)c * VEC, dyv[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) { xv[e] = 0.f; dyv[i][e] = 0.f; }
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        xh[i][e] = (live && c < nch) ? (xv[e] - mean) * rstd : 0.f;
+        wdy[i][e] = w[i][e] * dyv[i][e];
+        s1 += xh[i][e] * wdy[i][e];
+        s2 += wdy[i][e];
+      }
+    }
+    const float c1 = row_reduce(s1, Sum{}, tpr, red, slot) * inv_n;
+    const float c2 = row_reduce(s2, Sum{}, tpr, red, slot) * inv_n;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = t + i * tpr;
+        if (c < nch) {
+          float dx[VEC];
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            dx[e] = (wdy[i][e] - (xh[i][e] * c1 + c2)) * rstd;
+            dw[i][e] += dyv[i][e] * xh[i][e];
+            db[i][e] += dyv[i][e];
+          }
+          store_chunk<T, VEC>(DX + (size_t)row * ld + (size_t)c * VEC, dx);
+        }
+      }
+    }
+  }
+  // fold the row slots into slot 0 (fixed order: slot 0 + 1 + 2 + ...), 4 floats at a time
+  float* out = part + (size_t)blockIdx.x * 2 * N;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+#pragma unroll
+      for (int e0 = 0; e0 < VEC; e0 += 4) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (e0 + e < VEC) ? (which ? db[i][e0 + e] : dw[i][e0 + e]) : 0.f;
+        __syncthreads();  // previous round's reads are done
+        fold[threadIdx.x] = v;
+        __syncthreads();
+        if (rs == 0) {
+          for (int r = 1; r < rpb; ++r) v += fold[r * tpr + t];
+          const int c = t + i * tpr;
+          if (c < nch) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (e0 + e < VEC) out[(size_t)which * N + (size_t)c * VEC + e0 + e] = v[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Pass 2 (reference _layer_norm_bwd_dwdb :184-207): dw[n] = sum_g part[g][n],
+// db[n] = sum_g part[g][N + n], summed in a fixed order. Workgroup of 256 = 16
+// columns x 16 partial-row lanes; lane l loads partial rows l, l + 16, ...
+// (G <= 256: at most 16, all issued before the first add), then the 16 lane
+// sums are added in lane order through LDS.
+template <typename T>
+__global__ void __launch_bounds__(256)
+layernorm_dwdb_kernel(const float* __restrict__ part, T* __restrict__ DW, T* __restrict__ DB, int G, int N) {
+  __shared__ float acc[16][17];
+  const int col = threadIdx.x & 15, lane_g = threadIdx.x >> 4;
+  const int n2 = blockIdx.x * 16 + col;  // column of the [dw | db] row of length 2N
+  float v[BWD_MAX_GROUPS / 16];
+#pragma unroll
+  for (int j = 0; j < BWD_MAX_GROUPS / 16; ++j) {
+    const int g = lane_g + 16 * j;
+    v[j] = (n2 < 2 * N && g < G) ? part[(size_t)g * 2 * N + n2] : 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < BWD_MAX_GROUPS / 16; ++j) s += v[j];
+  acc[lane_g][col] = s;
+  __syncthreads();
+  if (lane_g == 0 && n2 < 2 * N) {
+    float t = acc[0][col];
+    for (int l = 1; l < 16; ++l) t += acc[l][col];
+    if (n2 < N) DW[n2] = from_f<T>(t);
+    else DB[n2 - N] = from_f<T>(t);
+  }
+}
+
+}  // namespace icpp_rows
+
+// ---------------------------------------------------------------------------
+// Host side: geometry choice, validation, dispatch
+// ---------------------------------------------------------------------------
+namespace icpp {
+int set_last_error(int code, const char* msg);  // icpp_abi.hip: the library's last-error buffer
+}
+
+namespace {
+
+using namespace icpp_rows;
+
+int set_error(int code, const char* msg) { return icpp::set_last_error(code, msg); }
+
+struct RowGeom {
+  int vec, tpr, cpt, block;
+};
+
+int next_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+int esize(int dtype) { return dtype == ICPP_F32 ? 4 : 2; }
+
+// Pick the chunk width, threads per row and chunks per thread for N columns.
+// Returns false when N needs more than cpt_max chunks for each of 1024 threads.
+bool row_geom(int N, int vec, int cpt_max, RowGeom* g) {
+  const int nch = (N + vec - 1) / vec;
+  int tpr = next_pow2((nch + cpt_max - 1) / cpt_max);
+  tpr = tpr < 64 ? 64 : tpr;
+  if (tpr > 1024) return false;
+  g->vec = vec;
+  g->tpr = tpr;
+  g->cpt = next_pow2((nch + tpr - 1) / tpr);
+  g->block = tpr >= 256 ? tpr : 256;
+  return true;
+}
+
+template <typename T, typename F>
+hipError_t dispatch_cpt(const RowGeom& g, F&& launch) {
+  // VEC = 16 / sizeof(T) or 1; CPT 1..16 (the geometry keeps CPT within the kernel's limits)
+  constexpr int V = 16 / (int)sizeof(T);
+  if (g.vec == V) {
+    switch (g.cpt) {
+      case 1: return launch(std::integral_constant<int, V>{}, std::integral_constant<int, 1>{});
+      case 2: return launch(std::integral_constant<int, V>{}, std::integral_constant<int, 2>{});
+      case 4: return launch(std::integral_constant<int, V>{}, std::integral_constant<int, 4>{});
+      default: return launch(std::integral_constant<int, V>{}, std::integral_constant<int, 8>{});
+    }
+  }
+  switch (g.cpt) {
+    case 1: return launch(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    case 2: return launch(std::integral_constant<int, 1>{}, std::integral_constant<int, 2>{});
+    case 4: return launch(std::integral_constant<int, 1>{}, std::integral_constant<int, 4>{});
+    case 8: return launch(std::integral_constant<int, 1>{}, std::integral_constant<int, 8>{});
+    default: return launch(std::integral_constant<int, 1>{}, std::integral_constant<int, 16>{});
+  }
+}
+
+template <typename T>
+int ln_fwd_t(const void* X, const void* W, const void* B, void* Y, float* mean, float* rstd, int M, int N, int ldx,
+             int ldy, float eps, hipStream_t s) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const bool vec_ok = N % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(X) && aligned16(Y) &&
+                      aligned16(W) && aligned16(B);
+  RowGeom g;
+  if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 8 : 16, &g)) return set_error(ICPP_E_SHAPE, "icpp_layernorm_fwd: N too large");
+  const int rpb = g.block / g.tpr;
+  const dim3 grid((M + rpb - 1) / rpb);
+  hipError_t e = dispatch_cpt<T>(g, [&](auto VEC, auto CPT) {
+    hipLaunchKernelGGL((layernorm_fwd_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), grid, dim3(g.block), 0, s,
+                       (const T*)X, (const T*)W, (const T*)B, (T*)Y, mean, rstd, M, N, ldx, ldy, eps, g.tpr);
+    return hipGetLastError();
+  });
+  return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
+}
+
+template <typename T>
+int softmax_t(const void* X, void* Y, int M, int N, int ldx, int ldy, hipStream_t s) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const bool vec_ok = N % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(X) && aligned16(Y);
+  RowGeom g;
+  if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 8 : 16, &g)) return set_error(ICPP_E_SHAPE, "icpp_softmax: N too large");
+  const int rpb = g.block / g.tpr;
+  const dim3 grid((M + rpb - 1) / rpb);
+  hipError_t e = dispatch_cpt<T>(g, [&](auto VEC, auto CPT) {
+    hipLaunchKernelGGL((softmax_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), grid, dim3(g.block), 0, s,
+                       (const T*)X, (T*)Y, M, N, ldx, ldy, g.tpr);
+    return hipGetLastError();
+  });
+  return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
+}
+
+// Backward geometry: w, dw, db and the row's x / dy / xhat / w*dy stay in
+// registers, and a 1024-thread workgroup leaves each wave 128 VGPRs: at most 2
+// chunks per thread (16 elements of a 16-bit type; N <= 16384) or 4 scalar ones.
+bool bwd_geom(int dtype, int N, int ld, bool ptrs_aligned, RowGeom* g) {
+  const int V = 16 / esize(dtype);
+  const bool vec_ok = N % V == 0 && ld % V == 0 && ptrs_aligned;
+  if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 2 : 4, g)) return false;
+  g->block = BWD_BLOCK;
+  return true;
+}
+
+int bwd_groups(int M, const RowGeom& g) {
+  const int rpb = g.block / g.tpr;
+  const int need = (M + rpb - 1) / rpb;
+  return need < BWD_MAX_GROUPS ? need : BWD_MAX_GROUPS;
+}
+
+template <typename T>
+int ln_bwd_t(const void* DY, const void* X, const void* W, const float* mean, const float* rstd, void* DX, void* DW,
+             void* DB, int M, int N, int ld, const RowGeom& g, float* part, hipStream_t s) {
+  const int G = bwd_groups(M, g);
+  hipError_t e = dispatch_cpt<T>(g, [&](auto VEC, auto CPT) {
+    if constexpr (decltype(CPT)::value > 4 || (decltype(VEC)::value > 1 && decltype(CPT)::value > 2)) {
+      return hipErrorInvalidValue;  // outside the backward's register budget (row_geom never picks it)
+    } else {
+      hipLaunchKernelGGL((layernorm_bwd_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), dim3(G), dim3(g.block),
+                         0, s, (const T*)DY, (const T*)X, (const T*)W, mean, rstd, (T*)DX, part, M, N, ld, g.tpr);
+      return hipGetLastError();
+    }
+  });
+  if (e != hipSuccess) return set_error((int)e, hipGetErrorString(e));
+  hipLaunchKernelGGL(layernorm_dwdb_kernel<T>, dim3((2 * N + 15) / 16), dim3(256), 0, s, part, (T*)DW, (T*)DB, G, N);
+  e = hipGetLastError();
+  return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
+}
+
+int check_rows(const char* fn, int dtype, int M, int N, int ld_in, int ld_out) {
+  if (dtype != ICPP_F16 && dtype != ICPP_BF16 && dtype != ICPP_F32)
+    return set_error(ICPP_E_ARG, fn);
+  if (M <= 0 || N <= 0 || ld_in < N || ld_out < N) return set_error(ICPP_E_SHAPE, fn);
+  if ((long long)M * ld_in > 0x7FFFFFFFll * 8 || (long long)M * ld_out > 0x7FFFFFFFll * 8)
+    return set_error(ICPP_E_SHAPE, fn);
+  return ICPP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int icpp_layernorm_fwd(int dtype, const void* X, const void* W, const void* B, void* Y, float* mean, float* rstd,
+                       int M, int N, int ldx, int ldy, float eps, void* stream) {
+  if (!X || !W || !B || !Y) return set_error(ICPP_E_ARG, "icpp_layernorm_fwd: null tensor");
+  if (int rc = check_rows("icpp_layernorm_fwd: bad dtype or shape", dtype, M, N, ldx, ldy)) return rc;
+  if (!(eps >= 0.f)) return set_error(ICPP_E_ARG, "icpp_layernorm_fwd: eps must be >= 0");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ICPP_F16) return ln_fwd_t<_Float16>(X, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
+  if (dtype == ICPP_BF16) return ln_fwd_t<__bf16>(X, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
+  return ln_fwd_t<float>(X, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
+}
+
+size_t icpp_layernorm_bwd_workspace_bytes(int dtype, int M, int N, int ld) {
+  // the larger of the 16-byte and per-element geometries: the call may take either
+  // (the pointers' alignment is not known here)
+  RowGeom g;
+  if (M <= 0 || N <= 0 || ld < N || !bwd_geom(dtype, N, ld, true, &g)) return 0;
+  int groups = bwd_groups(M, g);
+  RowGeom gs;
+  if (bwd_geom(dtype, N, ld, false, &gs) && bwd_groups(M, gs) > groups) groups = bwd_groups(M, gs);
+  return (size_t)groups * 2 * N * sizeof(float);
+}
+
+int icpp_layernorm_bwd(int dtype, const void* DY, const void* X, const void* W, const float* mean, const float* rstd,
+                       void* DX, void* DW, void* DB, int M, int N, int ld, void* workspace, size_t ws_bytes,
+                       void* stream) {
+  if (!DY || !X || !W || !mean || !rstd || !DX || !DW || !DB) return set_error(ICPP_E_ARG, "icpp_layernorm_bwd: null tensor");
+  if (int rc = check_rows("icpp_layernorm_bwd: bad dtype or shape", dtype, M, N, ld, ld)) return rc;
+  RowGeom g;
+  const bool al = aligned16(DY) && aligned16(X) && aligned16(W) && aligned16(DX);
+  if (!bwd_geom(dtype, N, ld, al, &g)) return set_error(ICPP_E_SHAPE, "icpp_layernorm_bwd: N too large");
+  const size_t need = (size_t)bwd_groups(M, g) * 2 * N * sizeof(float);
+  if (!workspace || ws_bytes < need || !aligned16(workspace))
+    return set_error(ICPP_E_WORKSPACE, "icpp_layernorm_bwd: workspace too small (see icpp_layernorm_bwd_workspace_bytes)");
+  hipStream_t s = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  if (dtype == ICPP_F16) return ln_bwd_t<_Float16>(DY, X, W, mean, rstd, DX, DW, DB, M, N, ld, g, part, s);
+  if (dtype == ICPP_BF16) return ln_bwd_t<__bf16>(DY, X, W, mean, rstd, DX, DW, DB, M, N, ld, g, part, s);
+  return ln_bwd_t<float>(DY, X, W, mean, rstd, DX, DW, DB, M, N, ld, g, part, s);
+}
+
+int icpp_softmax(int dtype, const void* X, void* Y, int M, int N, int ldx, int ldy, void* stream) {
+  if (!X || !Y) return set_error(ICPP_E_ARG, "icpp_softmax: null tensor");
+  if (int rc = check_rows("icpp_softmax: bad dtype or shape", dtype, M, N, ldx, ldy)) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ICPP_F16) return softmax_t<_Float16>(X, Y, M, N, ldx, ldy, s);
+  if (dtype == ICPP_BF16) return softmax_t<__bf16>(X, Y, M, N, ldx, ldy, s);
+  return softmax_t<float>(X, Y, M, N, ldx, ldy, s);
+}
+
+}  // extern "C"

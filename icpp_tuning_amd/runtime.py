@@ -12,7 +12,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import ACT, CONV_EPI, FAMILY, lib
+from ._lib import ACT, CONV_EPI, DTYPE, FAMILY, lib
 
 TORCH_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
 OUT_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.bfloat16}
@@ -138,5 +138,76 @@ def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, st
     return y
 
 
-__all__ = ["BIAS_DTYPE", "OUT_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
-           "gemm_bias_layernorm", "workspace_bytes"]
+ROW_DTYPE = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
+
+
+def _rows(x: torch.Tensor, name: str):
+    """A [M, N] view of x (last dimension = row) with unit column stride."""
+    if x.dtype not in ROW_DTYPE:
+        raise TypeError(f"{name} must be float16, bfloat16 or float32 (got {x.dtype})")
+    if not x.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (got {x.device})")
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        raise ValueError(f"{name} must have unit stride in its last dimension")
+    return x2
+
+
+def layernorm_fwd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5,
+                  out: Optional[torch.Tensor] = None):
+    """y = (x - mean) * rstd * weight + bias over the last dimension through icpp_layernorm_fwd;
+    returns (y, mean, rstd) with fp32 per-row statistics."""
+    x2 = _rows(x, "x")
+    M, N = x2.shape
+    dt = ROW_DTYPE[x.dtype]
+    pw, pb = _check(weight, "weight", x.dtype, (N,)), _check(bias, "bias", x.dtype, (N,))
+    if out is None:
+        out = torch.empty_like(x)
+    y2 = _rows(out, "out")
+    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    mean = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rstd = torch.empty((M,), dtype=torch.float32, device=x.device)
+    lib().call("icpp_layernorm_fwd", DTYPE[dt], x2.data_ptr(), pw, pb, y2.data_ptr(), mean.data_ptr(),
+               rstd.data_ptr(), M, N, x2.stride(0), y2.stride(0), float(eps), _stream())
+    return out, mean, rstd
+
+
+def layernorm_bwd(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, mean: torch.Tensor, rstd: torch.Tensor):
+    """(dx, dw, db) of the LayerNorm above through icpp_layernorm_bwd (dx in x's dtype and
+    layout; dw, db in weight's dtype)."""
+    x2 = _rows(x.contiguous(), "x")
+    dy2 = _rows(dy.contiguous(), "dy")
+    M, N = x2.shape
+    if tuple(dy2.shape) != (M, N) or dy.dtype != x.dtype:
+        raise ValueError("dy must match x")
+    dt = ROW_DTYPE[x.dtype]
+    pw = _check(weight, "weight", x.dtype, (N,))
+    pm = _check(mean, "mean", torch.float32, (M,))
+    pr = _check(rstd, "rstd", torch.float32, (M,))
+    dx = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    dw = torch.empty((N,), dtype=weight.dtype, device=x.device)
+    db = torch.empty((N,), dtype=weight.dtype, device=x.device)
+    need = lib().layernorm_bwd_workspace_bytes(DTYPE[dt], M, N, N)
+    ws = alloc_workspace(need, x.device)
+    lib().call("icpp_layernorm_bwd", DTYPE[dt], dy2.data_ptr(), x2.data_ptr(), pw, pm, pr, dx.data_ptr(),
+               dw.data_ptr(), db.data_ptr(), M, N, N, ws.data_ptr() if ws is not None else None, need, _stream())
+    return dx.reshape(x.shape), dw, db
+
+
+def softmax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Row-wise softmax over the last dimension through icpp_softmax (fp32 arithmetic)."""
+    x2 = _rows(x, "x")
+    M, N = x2.shape
+    if out is None:
+        out = torch.empty_like(x)
+    y2 = _rows(out, "out")
+    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    lib().call("icpp_softmax", DTYPE[ROW_DTYPE[x.dtype]], x2.data_ptr(), y2.data_ptr(), M, N, x2.stride(0),
+               y2.stride(0), _stream())
+    return out
+
+
+__all__ = ["BIAS_DTYPE", "OUT_DTYPE", "ROW_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
+           "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "softmax", "workspace_bytes"]

@@ -39,7 +39,7 @@ enum icpp_family {
   ICPP_NUM_FAMILIES = 4
 };
 
-enum icpp_dtype { ICPP_F16 = 0, ICPP_BF16 = 1, ICPP_FP8_E4M3 = 2 };
+enum icpp_dtype { ICPP_F16 = 0, ICPP_BF16 = 1, ICPP_FP8_E4M3 = 2, ICPP_F32 = 3 /* row ops only */ };
 enum icpp_act { ICPP_ACT_NONE = 0, ICPP_ACT_RELU = 1, ICPP_ACT_GELU_TANH = 2, ICPP_ACT_SILU = 3 };
 
 enum icpp_status {
@@ -137,6 +137,47 @@ int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, con
                            int N, int H, int W, int C, int F, int KH, int KW,
                            int stride, int pad, int dilation, int split_k,
                            void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Row operations over the last dimension of a row-major [M, N] tensor with row
+ * stride ld >= N (elements); dtype ICPP_F16, ICPP_BF16 or ICPP_F32, fp32
+ * arithmetic. The 16-byte path needs N, the strides and the pointers to be
+ * multiples of 16 bytes; otherwise a per-element path runs. Rows up to
+ * 8192 x (16 / element size) columns (16-byte path) or 16384 (per-element).
+ */
+
+/*
+ * Y = (X - mean) * rstd * W + B per row, rstd = 1 / sqrt(var + eps) with the
+ * centred (two-pass) variance; mean, rstd: [M] fp32 outputs (either may be
+ * null). Replaces _layer_norm_fwd_fused and LayerNorm.forward
+ * (kernel/triton/layernorm.py:48-91, :219-244).
+ */
+int icpp_layernorm_fwd(int dtype, const void* X, const void* W, const void* B, void* Y,
+                       float* mean, float* rstd, int M, int N, int ldx, int ldy, float eps,
+                       void* stream);
+
+/*
+ * Workspace bytes icpp_layernorm_bwd needs for these sizes (0 when N is beyond
+ * the backward's limit: 16384 columns of a 16-bit type, 8192 of f32, 4096 on
+ * the per-element path).
+ */
+size_t icpp_layernorm_bwd_workspace_bytes(int dtype, int M, int N, int ld);
+
+/*
+ * LayerNorm backward from the forward's mean / rstd: DX ([M, N], ld), DW, DB
+ * ([N], W's dtype). Replaces _layer_norm_bwd_dx_fused + _layer_norm_bwd_dwdb
+ * and LayerNorm.backward (layernorm.py:128-207, :246-275); dw / db are summed
+ * in fp32 in a fixed order (deterministic).
+ */
+int icpp_layernorm_bwd(int dtype, const void* DY, const void* X, const void* W,
+                       const float* mean, const float* rstd, void* DX, void* DW, void* DB,
+                       int M, int N, int ld, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Y = softmax(X) per row (exp(x - max) / sum). Replaces softmax_kernel and
+ * softmax (kernel/triton/softmax.py:32-55, :73-102).
+ */
+int icpp_softmax(int dtype, const void* X, void* Y, int M, int N, int ldx, int ldy, void* stream);
 
 #ifdef __cplusplus
 }

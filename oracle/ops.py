@@ -86,6 +86,45 @@ def conv2d_bn_act_ref(X, Wt, stride: int = 1, padding: int = 1, dilation: int = 
     return apply_act(y, act)
 
 
+def layernorm_fwd_ref(x, w, b, eps: float = 1e-5):
+    """Row LayerNorm in fp32 over the last dimension, as kernel/triton/layernorm.py
+    _layer_norm_fwd_fused (:64-91): mean, centred variance, rstd = 1/sqrt(var + eps),
+    y = (x - mean) * rstd * w + b.  Returns (y, mean, rstd)."""
+    x = x.float().cpu()
+    n = x.shape[-1]
+    mean = x.sum(-1) / n
+    d = x - mean.unsqueeze(-1)
+    var = (d * d).sum(-1) / n
+    rstd = 1.0 / torch.sqrt(var + eps)
+    y = d * rstd.unsqueeze(-1) * w.float().cpu() + b.float().cpu()
+    return y, mean, rstd
+
+
+def layernorm_bwd_ref(dy, x, w, mean, rstd):
+    """LayerNorm backward in fp32, as _layer_norm_bwd_dx_fused (:148-170) and
+    _layer_norm_bwd_dwdb (:194-207): xhat = (x - mean) * rstd, wdy = w * dy,
+    c1 = sum(xhat * wdy) / N, c2 = sum(wdy) / N, dx = (wdy - (xhat * c1 + c2)) * rstd,
+    dw = sum over rows of dy * xhat, db = sum over rows of dy.  Returns (dx, dw, db)."""
+    x = x.float().cpu().reshape(-1, x.shape[-1])
+    dy = dy.float().cpu().reshape(x.shape)
+    n = x.shape[-1]
+    xhat = (x - mean.float().cpu().unsqueeze(-1)) * rstd.float().cpu().unsqueeze(-1)
+    wdy = w.float().cpu() * dy
+    c1 = (xhat * wdy).sum(-1, keepdim=True) / n
+    c2 = wdy.sum(-1, keepdim=True) / n
+    dx = (wdy - (xhat * c1 + c2)) * rstd.float().cpu().unsqueeze(-1)
+    return dx, (dy * xhat).sum(0), dy.sum(0)
+
+
+def softmax_ref(x):
+    """Row softmax in fp32, as kernel/triton/softmax.py naive_softmax (:10-28):
+    z = x - max(x), exp(z) / sum(exp(z)) over the last dimension."""
+    x = x.float().cpu()
+    z = x - x.max(dim=-1, keepdim=True)[0]
+    num = torch.exp(z)
+    return num / num.sum(dim=-1, keepdim=True)
+
+
 def conv_out_hw(H, W, KH, KW, S, P, D=1):
     """reference conv2d.py:65-68"""
     return (H + 2 * P - D * (KH - 1) - 1) // S + 1, (W + 2 * P - D * (KW - 1) - 1) // S + 1

@@ -107,3 +107,30 @@ def test_fused_conv_validation_errors_before_launch(L):
     assert call(flags=RES, res=40) == -4                        # misaligned residual
     assert call(X=None) == -4
     assert "icpp_conv2d_nhwc" in L.last_error()
+
+
+def test_rowops_validation_errors_before_launch(L):
+    """icpp_layernorm_fwd / _bwd and icpp_softmax reject bad arguments before any
+    device work; the backward's workspace size follows one fp32 [dw | db] row per
+    workgroup (at most 256)."""
+    f16, f32 = _lib.DTYPE["f16"], _lib.DTYPE["f32"]
+    fwd, bwd, sm = L._dll.icpp_layernorm_fwd, L._dll.icpp_layernorm_bwd, L._dll.icpp_softmax
+    eps = ctypes.c_float(1e-5)
+    assert fwd(f16, None, 16, 16, 16, None, None, 4, 64, 64, 64, eps, None) == -4       # null x
+    assert fwd(9, 16, 16, 16, 16, None, None, 4, 64, 64, 64, eps, None) == -4          # bad dtype
+    assert fwd(f16, 16, 16, 16, 16, None, None, 4, 64, 32, 64, eps, None) == -2        # ld < N
+    assert fwd(f16, 16, 16, 16, 16, None, None, 0, 64, 64, 64, eps, None) == -2        # empty
+    assert fwd(f16, 16, 16, 16, 16, None, None, 4, 64, 64, 64, ctypes.c_float(-1.0), None) == -4
+    assert fwd(f16, 16, 16, 16, 16, None, None, 4, 1 << 17, 1 << 17, 1 << 17, eps, None) == -2  # row too long
+    assert sm(f32, None, 16, 4, 64, 64, 64, None) == -4
+    assert sm(f32, 16, 16, 4, 20000, 20001, 20001, None) == -2                        # scalar path limit 16384
+    ws = L.layernorm_bwd_workspace_bytes
+    # N = 8192 f16: 512 threads per row, 2 rows per 1024-thread workgroup
+    assert ws(f16, 4096, 8192, 8192) == 256 * 2 * 8192 * 4
+    assert ws(f16, 100, 8192, 8192) == 50 * 2 * 8192 * 4
+    assert ws(f16, 4096, 32768, 32768) == 0                                           # beyond the backward's limit
+    args = (f16, 16, 16, 16, 16, 16, 16, 16, 16, 4096, 8192, 8192)
+    assert bwd(*args, None, 0, None) == -3                                             # no workspace
+    assert bwd(*args, 16, 1024, None) == -3                                            # too small
+    assert bwd(f16, None, *args[2:], 16, 1 << 30, None) == -4                          # null dy
+    assert "icpp_layernorm_bwd" in L.last_error()

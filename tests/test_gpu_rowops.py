@@ -1,0 +1,150 @@
+"""GPU parity of the standalone row kernels (LayerNorm forward / backward, softmax)
+against the CPU oracle, through the C ABI (icpp_layernorm_fwd / _bwd, icpp_softmax).
+
+Tolerances, elementwise |got - want| <= atol + rtol |want|:
+  LayerNorm y, dx, dw, db   atol 1e-2 (the reference's test_layer_norm, layernorm.py:300-303)
+                            + rtol one unit in the last place of the storage type
+                            (2^-10 f16, 2^-7 bf16, 2^-20 f32): the reference's atol alone is
+                            below an ulp for the large |dw| of long columns
+  softmax f32               rtol 1e-5, atol 1e-8 (torch.allclose defaults, softmax.py:109)
+  softmax f16 / bf16        rtol one ulp, atol 1e-6
+Inputs follow the reference tests: x = -2.3 + 0.5 randn, w, b ~ U(0, 1), dy = 0.1 randn.
+"""
+
+import pytest
+import torch
+
+from icpp_tuning_amd import runtime
+from icpp_tuning_amd.kernels.layernorm import layer_norm
+from icpp_tuning_amd.kernels.softmax import softmax
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7, torch.float32: 2.0 ** -20}
+DT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _close(got, want, atol, rtol, what):
+    got = got.float().cpu()
+    want = want.float().cpu()
+    assert got.shape == want.shape, what
+    assert torch.isfinite(got).all(), f"{what}: non-finite"
+    err = (got - want).abs()
+    bad = err > atol + rtol * want.abs()
+    if bad.any():
+        idx = bad.nonzero()[0].tolist()
+        raise AssertionError(f"{what}: {int(bad.sum())} / {got.numel()} outside tol, max err {err.max().item():.4g}; "
+                             f"first at {idx}: got {got[tuple(idx)].item():.6g} want {want[tuple(idx)].item():.6g}")
+
+
+def _ln_inputs(M, N, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = (-2.3 + 0.5 * torch.randn(M, N, generator=g)).to(dtype)
+    w = torch.rand(N, generator=g).to(dtype)
+    b = torch.rand(N, generator=g).to(dtype)
+    dy = (0.1 * torch.randn(M, N, generator=g)).to(dtype)
+    return x, w, b, dy
+
+
+LN_CASES = [
+    # (M, N, dtype): the reference test (1151 x 8192 f16), bench-like rows, ragged / scalar-path N, tiny rows
+    (1151, 8192, "f16"),
+    (4096, 1024, "f16"),
+    (512, 15872, "f16"),
+    (333, 4096, "bf16"),
+    (257, 2048, "f32"),
+    (64, 781, "f16"),       # N % 8 != 0: per-element path
+    (7, 3, "f32"),
+    (1, 16384, "bf16"),
+    (3, 64, "f16"),
+]
+
+
+@pytest.mark.parametrize("M,N,dt", LN_CASES)
+def test_layernorm_fwd_bwd(gpu, M, N, dt):
+    dtype = DT[dt]
+    x, w, b, dy = _ln_inputs(M, N, dtype, 100 + M + N)
+    print(f"[parity] layernorm M={M} N={N} {dt}", flush=True)
+    y, mean, rstd = runtime.layernorm_fwd(x.cuda(), w.cuda(), b.cuda(), 1e-5)
+    dx, dw, db = runtime.layernorm_bwd(dy.cuda(), x.cuda(), w.cuda(), mean, rstd)
+    torch.cuda.synchronize()
+    y_ref, m_ref, r_ref = O.layernorm_fwd_ref(x, w, b, 1e-5)
+    dx_ref, dw_ref, db_ref = O.layernorm_bwd_ref(dy, x, w, m_ref, r_ref)
+    u = ULP[dtype]
+    _close(mean, m_ref, 1e-5, 1e-5, "mean")
+    _close(rstd, r_ref, 1e-5, 1e-4, "rstd")
+    _close(y, y_ref, 1e-2, u, f"y {M}x{N} {dt}")
+    _close(dx, dx_ref, 1e-2, u, f"dx {M}x{N} {dt}")
+    _close(dw, dw_ref, 1e-2, u, f"dw {M}x{N} {dt}")
+    _close(db, db_ref, 1e-2, u, f"db {M}x{N} {dt}")
+
+
+def test_layernorm_bwd_deterministic(gpu):
+    x, w, b, dy = [t.cuda() for t in _ln_inputs(3000, 4096, torch.float16, 7)]
+    _, mean, rstd = runtime.layernorm_fwd(x, w, b)
+    first = runtime.layernorm_bwd(dy, x, w, mean, rstd)
+    for _ in range(3):
+        again = runtime.layernorm_bwd(dy, x, w, mean, rstd)
+        for a, c in zip(first, again):
+            assert torch.equal(a, c)
+
+
+def test_layer_norm_autograd(gpu):
+    """The reference's usage (layernorm.py:282-303): layer_norm(x, w_shape, weight, bias, eps),
+    then y.backward(dy); compared with the oracle (atol 1e-2 as the reference's test)."""
+    M, N = 1151, 8192
+    x, w, b, dy = _ln_inputs(M, N, torch.float16, 11)
+    xc = x.cuda().requires_grad_(True)
+    wc = w.cuda().requires_grad_(True)
+    bc = b.cuda().requires_grad_(True)
+    y = layer_norm(xc, (N,), wc, bc, 1e-5)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    y_ref, m_ref, r_ref = O.layernorm_fwd_ref(x, w, b, 1e-5)
+    dx_ref, dw_ref, db_ref = O.layernorm_bwd_ref(dy, x, w, m_ref, r_ref)
+    u = ULP[torch.float16]
+    _close(y.detach(), y_ref, 1e-2, u, "y")
+    _close(xc.grad, dx_ref, 1e-2, u, "dx")
+    _close(wc.grad, dw_ref, 1e-2, u, "dw")
+    _close(bc.grad, db_ref, 1e-2, u, "db")
+
+
+SOFTMAX_CASES = [
+    (1823, 781, "f32"),     # the reference's test (softmax.py:104-108), per-element path
+    (4096, 4096, "f32"),
+    (4096, 12672, "f32"),   # the top of the reference's benchmark sweep
+    (1000, 1024, "f16"),
+    (300, 32768, "bf16"),
+    (5, 1, "f32"),
+    (2, 65536, "f16"),
+]
+
+
+@pytest.mark.parametrize("M,N,dt", SOFTMAX_CASES)
+def test_softmax(gpu, M, N, dt):
+    dtype = DT[dt]
+    g = torch.Generator().manual_seed(200 + N)
+    x = (3.0 * torch.randn(M, N, generator=g)).to(dtype)
+    print(f"[parity] softmax M={M} N={N} {dt}", flush=True)
+    y = softmax(x.cuda())
+    torch.cuda.synchronize()
+    want = O.softmax_ref(x)
+    if dtype == torch.float32:
+        _close(y, want, 1e-8, 1e-5, f"softmax {M}x{N}")
+    else:
+        _close(y, want, 1e-6, ULP[dtype], f"softmax {M}x{N} {dt}")
+
+
+def test_softmax_strided_rows(gpu):
+    """Rows of a wider buffer (row stride > N), as the reference's x.stride(0) argument allows."""
+    g = torch.Generator().manual_seed(5)
+    base = torch.randn(64, 1040, generator=g)
+    x = base[:, :1000]
+    y = torch.empty(64, 1000).cuda()
+    runtime.softmax(x.cuda().contiguous(), out=y)   # contiguous input
+    xs = base.cuda()[:, :1000]                      # strided input view
+    ys = runtime.softmax(xs)
+    torch.cuda.synchronize()
+    _close(ys, O.softmax_ref(x), 1e-8, 1e-5, "strided")
+    assert torch.equal(ys, y)

@@ -257,3 +257,58 @@ def test_conv_epilogue_rounds_conv_to_f16_first():
     ones = torch.ones(8)
     y = O.conv2d_bn_act_ref(X, Wt, 1, 0, bn=(2048 * ones, 0 * ones, ones, ones - eps), eps=eps)
     assert torch.equal(y, torch.zeros_like(y))
+
+
+# ---- standalone LayerNorm (forward, backward) and softmax ----
+
+def test_layernorm_fwd_ref_matches_torch_layer_norm():
+    g = torch.Generator().manual_seed(31)
+    x = -2.3 + 0.5 * torch.randn(37, 129, generator=g)     # the reference test's input distribution
+    w, b = torch.rand(129, generator=g), torch.rand(129, generator=g)
+    y, mean, rstd = O.layernorm_fwd_ref(x, w, b, 1e-5)
+    want = F.layer_norm(x.double(), (129,), w.double(), b.double(), 1e-5)
+    torch.testing.assert_close(y.double(), want, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(mean.double(), x.double().mean(-1), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(rstd.double(), 1 / torch.sqrt(x.double().var(-1, unbiased=False) + 1e-5),
+                               rtol=1e-5, atol=1e-5)
+
+
+def test_layernorm_bwd_ref_matches_autograd():
+    """dx, dw, db of the restated VJP against torch autograd of F.layer_norm in fp64."""
+    g = torch.Generator().manual_seed(32)
+    M, N = 23, 77
+    x = (-2.3 + 0.5 * torch.randn(M, N, generator=g)).double().requires_grad_(True)
+    w = torch.rand(N, generator=g).double().requires_grad_(True)
+    b = torch.rand(N, generator=g).double().requires_grad_(True)
+    dy = 0.1 * torch.randn(M, N, generator=g).double()
+    F.layer_norm(x, (N,), w, b, 1e-5).backward(dy)
+    _, mean, rstd = O.layernorm_fwd_ref(x.detach(), w.detach(), b.detach(), 1e-5)
+    dx, dw, db = O.layernorm_bwd_ref(dy, x.detach(), w.detach(), mean, rstd)
+    torch.testing.assert_close(dx.double(), x.grad, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(dw.double(), w.grad, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(db.double(), b.grad, rtol=1e-5, atol=1e-6)
+
+
+def test_layernorm_special_cases():
+    # constant rows: x - mean = 0 exactly, so y = b and dx = (w*dy - mean(w*dy)) * rstd
+    x = torch.full((3, 16), 1.75)
+    w, b = torch.linspace(0.5, 2.0, 16), torch.linspace(-1.0, 1.0, 16)
+    y, mean, rstd = O.layernorm_fwd_ref(x, w, b, 1e-5)
+    assert torch.equal(y, b.expand(3, 16))
+    assert torch.allclose(rstd, torch.full((3,), 1e-5 ** -0.5))
+    # dy = const, w = 1: dx = 0 (LayerNorm is shift invariant), db = M * const
+    xr = torch.randn(5, 8, generator=torch.Generator().manual_seed(3))
+    _, m2, r2 = O.layernorm_fwd_ref(xr, torch.ones(8), torch.zeros(8))
+    dx, dw, db = O.layernorm_bwd_ref(torch.full((5, 8), 0.25), xr, torch.ones(8), m2, r2)
+    assert dx.abs().max() < 1e-6 and torch.allclose(db, torch.full((8,), 1.25))
+    assert abs(float(dw.sum())) < 1e-5   # each row of xhat sums to 0, so with constant dy the columns of dw do too
+
+
+def test_softmax_ref_matches_torch_and_invariants():
+    g = torch.Generator().manual_seed(33)
+    x = torch.randn(19, 781, generator=g)                    # the reference test's row length
+    y = O.softmax_ref(x)
+    torch.testing.assert_close(y.double(), torch.softmax(x.double(), dim=1), rtol=1e-6, atol=1e-8)
+    torch.testing.assert_close(O.softmax_ref(x + 123.0), y, rtol=1e-5, atol=1e-8)   # shift invariance
+    assert torch.allclose(y.sum(-1), torch.ones(19), atol=1e-6)
+    assert torch.equal(O.softmax_ref(torch.zeros(2, 8)), torch.full((2, 8), 0.125))
