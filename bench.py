@@ -217,6 +217,51 @@ def bench_ops(quick: bool, only: str = ""):
         record_rows("layernorm_fwd", dict(M=4096, N=N), "f16", _ln(4096, N, False), 2 * 4096 * N * 2)
         record_rows("layernorm_bwd", dict(M=4096, N=N), "f16", _ln(4096, N, True), 3 * 4096 * N * 2)
 
+    # BERT encoder (reference evaluation/end2end.py bert_fwd_std, bert_base: 12 layers, 12 heads x 64):
+    # this library's GEMM blocks vs the same layer composed from torch ops, both on this GPU
+    def record_bert(batch, seq, layers=12):
+        op = "bert_base_e2e"
+        if only and not op.startswith(only):
+            return
+        import math as _m
+        import torch.nn.functional as TF
+
+        from icpp_tuning_amd.bert import BertLayer, BertLayerWeights, attention_core, bert_forward, causal_mask
+        heads, hs = 12, 64
+        H = heads * hs
+        ws = [BertLayerWeights.random(H, seed=i, device="cuda") for i in range(layers)]
+        g = torch.Generator(device="cuda").manual_seed(1)
+        x0 = (torch.rand(batch, seq, H, generator=g, device="cuda") * 0.8 - 0.4).half()
+        qkvs = [(torch.rand(batch, seq, 3 * H, generator=g, device="cuda") * 0.8 - 0.4).half() for _ in range(layers)]
+        mods = [BertLayer(w, batch, seq, heads, hs) for w in ws]
+        mask = causal_mask(seq, "cuda")
+
+        def torch_layers():
+            h0 = x0
+            for w, q in zip(ws, qkvs):
+                hh = attention_core(q + w.qkv_bias, heads, hs, mask,
+                                    softmax=lambda t: torch.softmax(t, dim=-1)).view(batch * seq, H)
+                x1 = TF.layer_norm(hh @ w.attr_output_kernel + w.attr_output_bias + h0.view(batch * seq, H), (H,),
+                                   w.attr_output_layernorm_gamma, w.attr_output_layernorm_beta)
+                it = TF.gelu(x1 @ w.inter_kernel + w.inter_bias)
+                h0 = TF.layer_norm(it @ w.output_kernel + w.output_bias + x1, (H,), w.output_layernorm_gamma,
+                                   w.output_layernorm_beta).view(batch, seq, H)
+            return h0
+
+        ms = benchmark_ms(lambda: bert_forward(mods, x0, qkvs), warmup=3, reps=10)
+        ms_t = benchmark_ms(torch_layers, warmup=3, reps=10)
+        flops = layers * 2.0 * batch * seq * (H * H + 8 * H * H) + layers * 4.0 * batch * heads * seq * seq * hs
+        rows.append({"op": op, "shape": dict(batch=batch, seq=seq, layers=layers), "dtype": "f16",
+                     "ms": round(ms, 4), "torch_composition_ms": round(ms_t, 4), "speedup": round(ms_t / ms, 3),
+                     "tflops": round(flops / ms / 1e9, 1)})
+        print(f"[bench] {op} b={batch} s={seq}: {ms:.3f} ms/iter (torch composition {ms_t:.3f} ms, "
+              f"x{ms_t / ms:.2f})", file=sys.stderr, flush=True)
+        del mods, ws, qkvs
+        torch.cuda.empty_cache()
+
+    for (bb, ss) in ([(1, 128)] if quick else [(1, 128), (32, 128), (8, 512)]):
+        record_bert(bb, ss)
+
     f8_shapes = [(16, 4096, 4096), (4096, 4096, 4096)] if quick else [
         (m, n, k) for m in (16, 256, 4096) for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008))]
     for (M, N, K) in f8_shapes:

@@ -22,13 +22,14 @@ FAMILY = {"gemm": 0, "gemm_ln_stats": 1, "gemm_ln_row": 2, "conv2d": 3}
 FAMILY_NAME = {v: k for k, v in FAMILY.items()}
 DTYPE = {"f16": 0, "bf16": 1, "fp8": 2, "f32": 3}
 DTYPE_NAME = {v: k for k, v in DTYPE.items()}
-ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu": 2, "silu": 3}
+ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu": 2, "silu": 3, "gelu_erf": 4}
 
 # every symbol declared in include/icpp_hip.h
 EXPORTED_SYMBOLS = (
     "icpp_abi_version", "icpp_last_error", "icpp_num_instances", "icpp_instance_info",
     "icpp_workspace_bytes", "icpp_gemm", "icpp_gemm_bias_layernorm", "icpp_conv2d_nhwc", "icpp_conv2d_nhwc_fused",
     "icpp_layernorm_fwd", "icpp_layernorm_bwd_workspace_bytes", "icpp_layernorm_bwd", "icpp_softmax",
+    "icpp_gemm_bias_residual_layernorm",
 )
 CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
@@ -62,6 +63,8 @@ _SIGNATURES = {
     "icpp_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "icpp_gemm": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp, _sz, _vp]),
     "icpp_gemm_bias_layernorm": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "icpp_gemm_bias_residual_layernorm": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz,
+                                               _vp]),
     "icpp_conv2d_nhwc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "icpp_conv2d_nhwc_fused": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _i, _i,
                                     _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),

@@ -257,7 +257,8 @@ PRIMITIVE_LIBRARY: Dict[str, FusionPrimitive] = {
     p.name: p for p in (BIAS_ADD, RELU, SILU, GELU, ROW_LAYERNORM, BATCHNORM)
 }
 # activation name used by the kernel ABI -> primitive name used by the scorer
-ACT_PRIMITIVE = {"none": None, "relu": "relu", "gelu_tanh": "gelu", "gelu": "gelu", "silu": "silu"}
+ACT_PRIMITIVE = {"none": None, "relu": "relu", "gelu_tanh": "gelu", "gelu": "gelu", "silu": "silu",
+                 "gelu_erf": "gelu"}
 
 
 def resolve_primitives(primitives: Iterable) -> Tuple[FusionPrimitive, ...]:

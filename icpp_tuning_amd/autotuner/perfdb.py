@@ -377,9 +377,12 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
     if op == "fp8_gemm_bias_silu":
         return build_sampling_plan(op, hw, m_range=(16, 4096), nk=[(4096, 4096), (11008, 4096), (4096, 11008)],
                                    points_per_wave=2)
-    if op == "gemm_bias_layernorm":
-        return build_sampling_plan(op, hw, m_range=(256, 8192), nk=[(768, 4096), (1024, 4096), (4096, 4096)],
+    if op == "gemm_bias_layernorm":   # C3 shapes, plus BERT-base's attention-output and FFN-output blocks
+        return build_sampling_plan(op, hw, m_range=(128, 8192),
+                                   nk=[(768, 4096), (1024, 4096), (4096, 4096), (768, 768), (768, 3072)],
                                    points_per_wave=2)
+    if op == "gemm_bias_gelu_erf":     # BERT-base's FFN-in block (end2end.py:82-83)
+        return build_sampling_plan(op, hw, m_range=(128, 16384), nk=[(3072, 768), (4096, 1024)], points_per_wave=2)
     return build_sampling_plan(op, hw, m_range=(16, 8192), nk=[(4096, 4096), (1024, 4096), (4096, 1024)],
                                points_per_wave=2)
 
@@ -387,8 +390,9 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
 def _descriptors():
     from ..kernels import conv2d, conv2d_fused, fp8_gemm_bias_act, gemm, gemm_bias_act, gemm_bias_layernorm
 
-    ds = [gemm.DESCRIPTOR, gemm_bias_act.descriptor("gelu_tanh", "bf16"), gemm_bias_layernorm.DESCRIPTOR,
-          fp8_gemm_bias_act.DESCRIPTOR, conv2d.DESCRIPTOR] + list(conv2d_fused.DESCRIPTORS.values())
+    ds = [gemm.DESCRIPTOR, gemm_bias_act.descriptor("gelu_tanh", "bf16"), gemm_bias_act.descriptor("gelu_erf", "f16"),
+          gemm_bias_layernorm.DESCRIPTOR, fp8_gemm_bias_act.DESCRIPTOR, conv2d.DESCRIPTOR] + \
+        list(conv2d_fused.DESCRIPTORS.values())
     return {d.name: d for d in ds}
 
 

@@ -1,0 +1,133 @@
+"""BERT encoder layer forward on the gfx950 fused kernels.
+
+Restates the reference's end-to-end harness layer (evaluation/end2end.py
+``bert_fwd_std`` :43-89) with its two GEMM blocks on this library:
+
+  attention output   LN(h @ Wo + bo + input)         icpp_gemm_bias_residual_layernorm  (:76-79)
+  FFN in             GELU(x @ Wi + bi)               icpp_gemm, act GELU-erf            (:82-83)
+  FFN out            LN(inter @ Wo2 + bo2 + x)       icpp_gemm_bias_residual_layernorm  (:84-87)
+
+The attention core (:52-71: scores = q k^T / sqrt(d) + causal mask, softmax,
+attention @ v) runs as in the reference -- two batched library GEMMs -- with
+the row softmax of this library; dropout is p = 0 there (:230).  Like the
+reference, the layer takes the QKV projections as given activations
+(``qkv_kernel[layer] + qkv_bias[layer]``, :47) rather than computing them.
+
+The reference imports helpers from a ``util`` package it does not ship
+(``transpose_for_scores``, ``set_dtype``, ``time_stamp_cudasync``, ...); the
+two this layer needs are restated below.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+
+from . import runtime
+from .kernels import gemm_bias_act, gemm_bias_layernorm
+
+
+def transpose_for_scores(x: torch.Tensor, head_num: int, head_size: int) -> torch.Tensor:
+    """[b, s, head_num * head_size] -> [b, s, head_num, head_size] (the reference's util helper,
+    used at end2end.py:49-51 before its permute(0, 2, 1, 3))."""
+    return x.view(x.shape[0], x.shape[1], head_num, head_size)
+
+
+def causal_mask(seq_len: int, device, dtype=torch.float16) -> torch.Tensor:
+    """Additive mask: -10000 above the diagonal, 0 elsewhere (end2end.py:62)."""
+    return torch.triu(torch.full((seq_len, seq_len), -10000.0, device=device), 1).to(dtype)
+
+
+@dataclass
+class BertLayerWeights:
+    """One layer's parameters, names as the reference's lists (end2end.py:276-286)."""
+    qkv_bias: torch.Tensor                     # [3H]
+    attr_output_kernel: torch.Tensor           # [H, H]
+    attr_output_bias: torch.Tensor             # [H]
+    attr_output_layernorm_gamma: torch.Tensor  # [H]
+    attr_output_layernorm_beta: torch.Tensor   # [H]
+    inter_kernel: torch.Tensor                 # [H, 4H]
+    inter_bias: torch.Tensor                   # [4H]
+    output_kernel: torch.Tensor                # [4H, H]
+    output_bias: torch.Tensor                  # [H]
+    output_layernorm_gamma: torch.Tensor       # [H]
+    output_layernorm_beta: torch.Tensor        # [H]
+
+    @staticmethod
+    def random(hidden: int, seed: int, device="cpu", dtype=torch.float16) -> "BertLayerWeights":
+        """U(-0.4, 0.4) for every parameter, as the reference initialises them."""
+        g = torch.Generator().manual_seed(seed)
+
+        def u(*shape):
+            return (torch.rand(*shape, generator=g) * 0.8 - 0.4).to(dtype).to(device)
+
+        H = hidden
+        return BertLayerWeights(u(3 * H), u(H, H), u(H), u(H), u(H), u(H, 4 * H), u(4 * H), u(4 * H, H), u(H), u(H), u(H))
+
+    def to(self, device) -> "BertLayerWeights":
+        return BertLayerWeights(*[getattr(self, f).to(device) for f in self.__dataclass_fields__])
+
+
+def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch.Tensor,
+                   softmax=runtime.softmax) -> torch.Tensor:
+    """softmax(q k^T / sqrt(d) + mask) v over heads, [b, s, 3H] -> [b, s, H] (end2end.py:47-71).
+    The batched products run in torch (with contiguous operands); the softmax is icpp_softmax
+    unless another row softmax is given."""
+    b, s, _ = qkv.shape
+    H = head_num * head_size
+    q1, k1, v1 = qkv.chunk(3, dim=-1)
+    q = transpose_for_scores(q1, head_num, head_size).permute(0, 2, 1, 3).reshape(b * head_num, s, head_size).contiguous()
+    k = transpose_for_scores(k1, head_num, head_size).permute(0, 2, 3, 1).reshape(b * head_num, head_size, s).contiguous()
+    v = transpose_for_scores(v1, head_num, head_size).permute(0, 2, 1, 3).reshape(b * head_num, s, head_size).contiguous()
+    scores = torch.bmm(q, k) * (1.0 / math.sqrt(head_size))
+    scores = (scores.view(b, head_num, s, s) + mask).reshape(b * head_num * s, s)
+    attn = softmax(scores.contiguous()).view(b * head_num, s, s)
+    h = torch.bmm(attn, v)                                       # [b*h, s, d]
+    return h.view(b, head_num, s, head_size).permute(0, 2, 1, 3).reshape(b, s, H).contiguous()
+
+
+class BertLayer:
+    """One encoder layer at a fixed (batch, seq_len): the three GEMM blocks are
+    resolved to compiled instances once (adaptive select), then ``forward``
+    launches them."""
+
+    def __init__(self, weights: BertLayerWeights, batch: int, seq_len: int, head_num: int = 12, head_size: int = 64,
+                 eps: float = 1e-5):
+        H = head_num * head_size
+        M = batch * seq_len
+        self.w, self.batch, self.seq, self.heads, self.hsize, self.eps = weights, batch, seq_len, head_num, head_size, eps
+        self.attn_out = gemm_bias_layernorm.build_fused_kernel(M, H, H, eps=eps)
+        self.ffn_in = gemm_bias_act.build_kernel(M, 4 * H, H, act="gelu_erf", dtype="f16")
+        self.ffn_out = gemm_bias_layernorm.build_fused_kernel(M, H, 4 * H, eps=eps)
+        self._mask: Optional[torch.Tensor] = None
+
+    def forward(self, qkv_kernel: torch.Tensor, input_tensor: torch.Tensor) -> torch.Tensor:
+        """qkv_kernel: [b, s, 3H] projections (the layer adds qkv_bias); input_tensor: [b, s, H]."""
+        w = self.w
+        b, s = self.batch, self.seq
+        H = self.heads * self.hsize
+        if self._mask is None or self._mask.device != qkv_kernel.device:
+            self._mask = causal_mask(s, qkv_kernel.device, qkv_kernel.dtype)
+        qkv = qkv_kernel + w.qkv_bias
+        h = attention_core(qkv, self.heads, self.hsize, self._mask).view(b * s, H)
+        x1 = self.attn_out(h, w.attr_output_kernel, w.attr_output_bias, w.attr_output_layernorm_gamma,
+                           w.attr_output_layernorm_beta, residual=input_tensor.reshape(b * s, H))
+        inter = self.ffn_in(x1, w.inter_kernel, w.inter_bias)
+        out = self.ffn_out(inter, w.output_kernel, w.output_bias, w.output_layernorm_gamma, w.output_layernorm_beta,
+                           residual=x1)
+        return out.view(b, s, H)
+
+
+def bert_forward(layers: List[BertLayer], input_from_tensor: torch.Tensor, qkv_kernels: List[torch.Tensor]):
+    """The reference's layer loop (end2end.py:45-89): each layer's output feeds the next
+    layer's residual input; the QKV activations are given per layer."""
+    hidden = input_from_tensor
+    for layer, qkv in zip(layers, qkv_kernels):
+        hidden = layer.forward(qkv, hidden)
+    return hidden
+
+
+__all__ = ["BertLayer", "BertLayerWeights", "attention_core", "bert_forward", "causal_mask", "transpose_for_scores"]

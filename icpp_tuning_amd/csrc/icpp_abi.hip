@@ -154,7 +154,7 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
   const icpp_tile_t& t = in->tile;
   if (!A || !B || !C) return fail(ICPP_E_ARG, "icpp_gemm: null tensor");
   if (M <= 0 || N <= 0 || K <= 0) return fail(ICPP_E_SHAPE, "icpp_gemm: empty shape M=%d N=%d K=%d", M, N, K);
-  if (act < ICPP_ACT_NONE || act > ICPP_ACT_SILU) return fail(ICPP_E_ARG, "icpp_gemm: bad act %d", act);
+  if (act < ICPP_ACT_NONE || act > ICPP_ACT_GELU_ERF) return fail(ICPP_E_ARG, "icpp_gemm: bad act %d", act);
   if (split_k < 1) return fail(ICPP_E_ARG, "icpp_gemm: split_k=%d", split_k);
   const int e = esz_of(t.dtype);
   const int vec = 16 / e;
@@ -196,6 +196,14 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
                              const void* gamma, const void* beta, void* Y,
                              int M, int N, int K, float eps,
                              void* workspace, size_t ws_bytes, void* stream) {
+  return icpp_gemm_bias_residual_layernorm(family, inst, A, B, bias, nullptr, gamma, beta, Y, M, N, K, eps,
+                                           workspace, ws_bytes, stream);
+}
+
+int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
+                                      const void* residual, const void* gamma, const void* beta, void* Y,
+                                      int M, int N, int K, float eps,
+                                      void* workspace, size_t ws_bytes, void* stream) {
   if (family != ICPP_FAMILY_GEMM_LN_ROW && family != ICPP_FAMILY_GEMM_LN_STATS)
     return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: family %d is not a LayerNorm family", family);
   const Instance* in = lookup(family, inst);
@@ -205,11 +213,12 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
   if (M <= 0 || N <= 0 || K <= 0) return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: empty shape");
   if (N % 8 || K % 8) return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: need N%%8==0 and K%%8==0");
   if (K % t.block_k) return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: K=%d not a multiple of block_k=%d", K, t.block_k);
-  if (!aligned16(A) || !aligned16(B) || !aligned16(Y) || !aligned16(gamma) || !aligned16(beta) || (bias && !aligned16(bias)))
+  if (!aligned16(A) || !aligned16(B) || !aligned16(Y) || !aligned16(gamma) || !aligned16(beta) || (bias && !aligned16(bias)) ||
+      (residual && !aligned16(residual)))
     return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: pointers must be 16-byte aligned");
   if (!(eps > 0.f)) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: eps must be > 0");
   KArgs a = base_args();
-  a.A = A; a.B = B; a.bias = bias; a.C = Y; a.gamma = gamma; a.beta = beta;
+  a.A = A; a.B = B; a.bias = bias; a.C = Y; a.gamma = gamma; a.beta = beta; a.residual = residual;
   a.M = M; a.N = N; a.K = K; a.lda = K; a.ldb = N; a.ldc = N; a.eps = eps;
   a.k_split = K;
   a.splits = 1;

@@ -37,7 +37,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 enum DType { DT_F16 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_F32 = 3 };
-enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3 };
+enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3, ACT_GELU_ERF = 4 };
 enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
 // A operand loaders: dense rows, the NHWC implicit-GEMM gather for any C
 // (per 16-byte chunk), and the gather for C % BK == 0, where every K tile is one
@@ -95,6 +95,7 @@ struct KArgs {
   int cH, cW, cC, cKH, cKW, cS, cP, cD, cOH, cOW;
   uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
   ConvEpiArgs ce;          // fused conv epilogue (conv instances only)
+  const void* residual;    // LayerNorm epilogues: [M, ldc] (output type) added before the statistics, or null
 };
 
 template <int DT> struct DTraits;
@@ -203,6 +204,7 @@ __device__ __forceinline__ i32x2 lds_tr8(const char ICPP_LDS* base, uint32_t off
 // once per activation and picked with one uniform switch per tile):
 //   GELU-tanh(x) = 0.5 x (1 + tanh(u)) = x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
 //   SiLU(x)      = x * sigmoid(x)
+//   GELU-erf(x)  = 0.5 x (1 + erf(x / sqrt(2)))  (erff: the device library's, ~2 ulp)
 // sigmoid(z) = 1 / (1 + exp(-z)) with the hardware exp2 and reciprocal
 // (v_exp_f32, v_rcp_f32: ~1 ulp each) instead of an IEEE division; z -> -inf
 // gives rcp(inf) = 0, so x * sigmoid stays finite.
@@ -212,6 +214,7 @@ __device__ __forceinline__ float act_fn(float x) {
   if constexpr (ACT == ACT_RELU) return fmaxf(x, 0.f);
   else if constexpr (ACT == ACT_GELU_TANH) return x * fast_sigmoid(1.5957691216057308f * (x + 0.044715f * x * x * x));
   else if constexpr (ACT == ACT_SILU) return x * fast_sigmoid(x);
+  else if constexpr (ACT == ACT_GELU_ERF) return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
   else return x;
 }
 // f(std::integral_constant<int, act>) for the runtime activation code act
@@ -221,6 +224,7 @@ __device__ __forceinline__ void dispatch_act(int act, F&& f) {
     case ACT_RELU: f(std::integral_constant<int, ACT_RELU>{}); break;
     case ACT_GELU_TANH: f(std::integral_constant<int, ACT_GELU_TANH>{}); break;
     case ACT_SILU: f(std::integral_constant<int, ACT_SILU>{}); break;
+    case ACT_GELU_ERF: f(std::integral_constant<int, ACT_GELU_ERF>{}); break;
     default: f(std::integral_constant<int, ACT_NONE>{}); break;
   }
 }
@@ -903,9 +907,10 @@ gemm_kernel(KArgs p) {
         });
       }
     } else {
-      // LayerNorm epilogues: x = acc + bias, statistics over valid columns (n < N)
+      // LayerNorm epilogues: x = acc + bias (+ residual), statistics over valid columns (n < N)
       OutT* C = (OutT*)p.C;
       const BiasT* bias = (const BiasT*)p.bias;
+      const OutT* res = (const OutT*)p.residual;
       float xs[G::TM][G::TN][Op::ACC];
 #pragma unroll
       for (int tn = 0; tn < G::TN; ++tn)
@@ -920,6 +925,26 @@ gemm_kernel(KArgs p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] = ok ? (acc[tm][tn][4 * g + e] + bv[e]) : 0.f;
         }
+      if (res != nullptr) {
+        // one row band's loads at a time (a scheduling barrier per band): the largest
+        // tiles have no registers left for every band's residual in flight
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          const int m = out_row(tm);
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+              const int n = out_col(tn, g);
+              if (n < p.N && m < p.M) {
+                const f32x4 rv = Vec4Store<OutT>::ld(res + (size_t)m * p.ldc + n);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] += rv[e];
+              }
+            }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
       // row sums over this wave's columns, reduced across the lanes sharing a row
       auto lane_reduce = [&](float v) ICPP_INLINE {
         if (MF == 16) {

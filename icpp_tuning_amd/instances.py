@@ -166,6 +166,11 @@ def _ln_tiles() -> List[Inst]:
         _g("f16", 128, 256, 64, 2, 4, 16, fam=st),
         _g("f16", 128, 128, 64, 2, 2, 16, st=3, fam=st),
         _g("f16", 128, 128, 32, 2, 2, 16, st=4, fam=st),
+        # small tiles: short activations (BERT's M = batch x seq from 128) still fill the CUs
+        _g("f16", 64, 64, 64, 2, 2, 16, fam=st),
+        _g("f16", 64, 64, 64, 2, 2, 16, st=4, fam=st),
+        _g("f16", 64, 128, 64, 1, 4, 16, fam=st),
+        _g("f16", 32, 128, 64, 1, 4, 16, fam=st),
         _g("f16", 32, 768, 32, 1, 8, 16, fam=row),
         _g("f16", 64, 768, 32, 1, 8, 16, fam=row),
         _g("f16", 32, 1024, 32, 1, 8, 16, fam=row),

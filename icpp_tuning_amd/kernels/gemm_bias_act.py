@@ -19,7 +19,7 @@ from .. import inputs as _inputs
 from ._base import InstanceDescriptor
 from .gemm import CompiledGemm
 
-ACTIVATIONS = ("relu", "gelu_tanh", "silu")
+ACTIVATIONS = ("relu", "gelu_tanh", "silu", "gelu_erf")   # gelu_erf: torch's default F.gelu (end2end.py:83)
 
 
 class GemmBiasActDescriptor(InstanceDescriptor):

@@ -108,12 +108,14 @@ class CompiledGemmLayerNorm:
         self.inst = DESCRIPTOR.instance_index(config)
         self._ws: Optional[torch.Tensor] = None
 
-    def __call__(self, A, B, bias, gamma, beta, out=None):
+    def __call__(self, A, B, bias, gamma, beta, out=None, residual=None):
+        """``LayerNorm(A @ B + bias [+ residual]) * gamma + beta``; the residual ([M, N] f16, may be
+        ``out``) is the add of the BERT attention-output / FFN-output blocks (end2end.py:76-79)."""
         need = runtime.workspace_bytes(self.family, self.inst, self.M, self.N, self.K)
         if need and (self._ws is None or self._ws.device != A.device):
             self._ws = runtime.alloc_workspace(need, A.device)
         return runtime.gemm_bias_layernorm(self.family, self.inst, A, B, bias, gamma, beta, out=out,
-                                           eps=self.eps, workspace=self._ws)
+                                           eps=self.eps, workspace=self._ws, residual=residual)
 
 
 def build_fused_kernel(M, N, K, gemm_config=None, block_M_ln=16, block_N_ln=128, thread_num_ln=128, eps=1e-5):

@@ -74,8 +74,10 @@ def gemm(inst: int, dtype: str, a: torch.Tensor, b: torch.Tensor, bias: Optional
 
 def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor, bias: Optional[torch.Tensor],
                         gamma: torch.Tensor, beta: torch.Tensor, out: Optional[torch.Tensor] = None,
-                        eps: float = 1e-5, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out = LayerNorm_N(a @ b + bias) * gamma + beta through icpp_gemm_bias_layernorm (f16)."""
+                        eps: float = 1e-5, workspace: Optional[torch.Tensor] = None,
+                        residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = LayerNorm_N(a @ b + bias [+ residual]) * gamma + beta through icpp_gemm_bias_layernorm
+    (or icpp_gemm_bias_residual_layernorm with a residual [M, N] f16; it may be out itself)."""
     M, K = a.shape
     _, N = b.shape
     h = torch.float16
@@ -90,8 +92,13 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
         workspace = alloc_workspace(need, a.device)
     pws = workspace.data_ptr() if (need and workspace is not None) else None
     wsb = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
-    lib().call("icpp_gemm_bias_layernorm", FAMILY[family], inst, pa, pb, pbias, pg, pbe, py,
-               M, N, K, float(eps), pws, wsb, _stream())
+    if residual is None:
+        lib().call("icpp_gemm_bias_layernorm", FAMILY[family], inst, pa, pb, pbias, pg, pbe, py,
+                   M, N, K, float(eps), pws, wsb, _stream())
+    else:
+        pr = _check(residual, "residual", h, (M, N))
+        lib().call("icpp_gemm_bias_residual_layernorm", FAMILY[family], inst, pa, pb, pbias, pr, pg, pbe, py,
+                   M, N, K, float(eps), pws, wsb, _stream())
     return out
 
 

@@ -40,7 +40,8 @@ enum icpp_family {
 };
 
 enum icpp_dtype { ICPP_F16 = 0, ICPP_BF16 = 1, ICPP_FP8_E4M3 = 2, ICPP_F32 = 3 /* row ops only */ };
-enum icpp_act { ICPP_ACT_NONE = 0, ICPP_ACT_RELU = 1, ICPP_ACT_GELU_TANH = 2, ICPP_ACT_SILU = 3 };
+enum icpp_act { ICPP_ACT_NONE = 0, ICPP_ACT_RELU = 1, ICPP_ACT_GELU_TANH = 2, ICPP_ACT_SILU = 3,
+                ICPP_ACT_GELU_ERF = 4 /* 0.5 x (1 + erf(x / sqrt 2)), torch's default F.gelu */ };
 
 enum icpp_status {
   ICPP_OK = 0,
@@ -98,6 +99,18 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
                              const void* gamma, const void* beta, void* Y,
                              int M, int N, int K, float eps,
                              void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Y = LayerNorm_N(A[M,K] @ B[K,N] + bias + residual) * gamma + beta: the
+ * attention-output and FFN-output blocks of the reference's BERT layer
+ * (evaluation/end2end.py:76-79, :84-87: matmul + bias, + residual, F.layer_norm).
+ * residual is [M, N] f16 (may be Y itself: each element is read before it is
+ * written, by the same lane); null gives icpp_gemm_bias_layernorm.
+ */
+int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
+                                      const void* residual, const void* gamma, const void* beta, void* Y,
+                                      int M, int N, int K, float eps,
+                                      void* workspace, size_t ws_bytes, void* stream);
 
 /*
  * Y[N,OH,OW,F] = conv2d(X[N,H,W,C], W[KH,KW,C,F]), f16, fp32 accumulate.

@@ -33,6 +33,8 @@ def apply_act(x: torch.Tensor, act: str) -> torch.Tensor:
         return gelu_tanh(x)
     if act == "silu":
         return x * torch.sigmoid(x)                    # SiLU = x * sigmoid(x)
+    if act == "gelu_erf":
+        return 0.5 * x * (1.0 + torch.erf(x * (1.0 / math.sqrt(2.0))))   # F.gelu (end2end.py:83)
     raise ValueError(act)
 
 
@@ -45,12 +47,15 @@ def gemm_bias_act_ref(A, B, bias, act: str = "relu") -> torch.Tensor:
     return apply_act(x, act)
 
 
-def gemm_bias_layernorm_ref(A, B, bias, gamma, beta, eps: float = 1e-5) -> torch.Tensor:
+def gemm_bias_layernorm_ref(A, B, bias, gamma, beta, eps: float = 1e-5, residual=None) -> torch.Tensor:
     """layer_norm(A @ B + bias, (N,), gamma, beta, eps) in fp32 -- reference
-    gemm_bias_layernorm.py:43-49 (torch_baseline)."""
+    gemm_bias_layernorm.py:43-49 (torch_baseline); with a residual, layer_norm(A @ B +
+    bias + residual) as the BERT attention-output / FFN-output blocks (end2end.py:76-79, :84-87)."""
     x = gemm_ref(A, B)
     if bias is not None:
         x = x + bias.float().cpu().unsqueeze(0)
+    if residual is not None:
+        x = x + residual.float().cpu()
     mean = x.mean(dim=1, keepdim=True)
     var = ((x - mean) ** 2).mean(dim=1, keepdim=True)  # biased variance, two-pass
     return (x - mean) * torch.rsqrt(var + eps) * gamma.float().cpu() + beta.float().cpu()
@@ -123,6 +128,32 @@ def softmax_ref(x):
     z = x - x.max(dim=-1, keepdim=True)[0]
     num = torch.exp(z)
     return num / num.sum(dim=-1, keepdim=True)
+
+
+def bert_layer_ref(qkv_kernel, input_tensor, w, head_num: int, head_size: int, eps: float = 1e-5):
+    """One BERT encoder layer in fp32, as evaluation/end2end.py bert_fwd_std (:47-87):
+    qkv = qkv_kernel + qkv_bias; per head scores = q k^T / sqrt(d) + causal mask
+    (-10000 above the diagonal), softmax, @ v; x = LN(h @ Wo + bo + input);
+    out = LN(gelu_erf(x @ Wi + bi) @ Wo2 + bo2 + x).  w: a BertLayerWeights-like object."""
+    f = lambda t: t.float().cpu()  # noqa: E731
+    b, s, _ = qkv_kernel.shape
+    H = head_num * head_size
+    qkv = f(qkv_kernel) + f(w.qkv_bias)
+    q, k, v = (t.reshape(b, s, head_num, head_size).permute(0, 2, 1, 3) for t in qkv.chunk(3, dim=-1))
+    scores = (q @ k.transpose(-1, -2)) / math.sqrt(head_size)
+    scores = scores + torch.triu(torch.full((s, s), -10000.0), 1)
+    h = (softmax_ref(scores) @ v).permute(0, 2, 1, 3).reshape(b * s, H)
+
+    def ln(x, g, be):
+        mean = x.mean(-1, keepdim=True)
+        var = ((x - mean) ** 2).mean(-1, keepdim=True)
+        return (x - mean) * torch.rsqrt(var + eps) * f(g) + f(be)
+
+    x1 = ln(h @ f(w.attr_output_kernel) + f(w.attr_output_bias) + f(input_tensor).reshape(b * s, H),
+            w.attr_output_layernorm_gamma, w.attr_output_layernorm_beta)
+    inter = apply_act(x1 @ f(w.inter_kernel) + f(w.inter_bias), "gelu_erf")
+    out = ln(inter @ f(w.output_kernel) + f(w.output_bias) + x1, w.output_layernorm_gamma, w.output_layernorm_beta)
+    return out.reshape(b, s, H)
 
 
 def conv_out_hw(H, W, KH, KW, S, P, D=1):

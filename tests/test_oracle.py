@@ -312,3 +312,54 @@ def test_softmax_ref_matches_torch_and_invariants():
     torch.testing.assert_close(O.softmax_ref(x + 123.0), y, rtol=1e-5, atol=1e-8)   # shift invariance
     assert torch.allclose(y.sum(-1), torch.ones(19), atol=1e-6)
     assert torch.equal(O.softmax_ref(torch.zeros(2, 8)), torch.full((2, 8), 0.125))
+
+
+def test_gelu_erf_matches_math_erf_and_torch():
+    """GELU-erf against math.erf element by element (fp64) and torch's default F.gelu."""
+    x = torch.linspace(-6, 6, 241)
+    want = torch.tensor([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x.double().tolist()], dtype=torch.float64)
+    torch.testing.assert_close(O.apply_act(x.double(), "gelu_erf"), want, rtol=1e-12, atol=1e-15)
+    got = O.apply_act(x, "gelu_erf")
+    torch.testing.assert_close(got, F.gelu(x), rtol=1e-6, atol=1e-6)
+    # differs from the tanh form (the two must not be confused): max gap ~1e-3 around |x| ~ 2
+    assert (got - O.apply_act(x, "gelu_tanh")).abs().max() > 1e-4
+
+
+def test_residual_layernorm_ref():
+    """LN(A@B + bias + residual): equals the no-residual oracle on (A@B + residual) when the
+    residual is folded into the bias row by row, and matches torch's layer_norm in fp64."""
+    g = torch.Generator().manual_seed(41)
+    A, B = torch.randn(9, 32, generator=g).half(), (0.1 * torch.randn(32, 24, generator=g)).half()
+    bias, R = torch.randn(24, generator=g).half(), torch.randn(9, 24, generator=g).half()
+    gamma, beta = torch.rand(24, generator=g).half(), torch.rand(24, generator=g).half()
+    got = O.gemm_bias_layernorm_ref(A, B, bias, gamma, beta, 1e-5, residual=R)
+    x = A.double() @ B.double() + bias.double() + R.double()
+    want = F.layer_norm(x, (24,), gamma.double(), beta.double(), 1e-5)
+    torch.testing.assert_close(got.double(), want, rtol=1e-5, atol=1e-5)
+    # a residual of zeros is the plain GEMM+bias+LN
+    torch.testing.assert_close(O.gemm_bias_layernorm_ref(A, B, bias, gamma, beta, 1e-5, residual=0 * R),
+                               O.gemm_bias_layernorm_ref(A, B, bias, gamma, beta, 1e-5), rtol=0, atol=0)
+
+
+def test_bert_layer_ref_matches_sdpa_composition():
+    """The BERT layer oracle against an independent fp64 composition: torch's
+    scaled_dot_product_attention with the additive causal mask, F.layer_norm, F.gelu."""
+    from icpp_tuning_amd.bert import BertLayerWeights
+
+    b, s, heads, d = 2, 16, 4, 16
+    H = heads * d
+    w = BertLayerWeights.random(H, seed=5, dtype=torch.float32)
+    g = torch.Generator().manual_seed(6)
+    qkv = torch.rand(b, s, 3 * H, generator=g) * 0.8 - 0.4
+    x0 = torch.rand(b, s, H, generator=g) * 0.8 - 0.4
+    got = O.bert_layer_ref(qkv, x0, w, heads, d)
+    D = lambda t: t.double()  # noqa: E731
+    q, k, v = (t.reshape(b, s, heads, d).permute(0, 2, 1, 3) for t in (D(qkv) + D(w.qkv_bias)).chunk(3, -1))
+    mask = torch.triu(torch.full((s, s), -10000.0, dtype=torch.float64), 1)
+    h = F.scaled_dot_product_attention(q, k, v, attn_mask=mask).permute(0, 2, 1, 3).reshape(b, s, H)
+    x1 = F.layer_norm(h @ D(w.attr_output_kernel) + D(w.attr_output_bias) + D(x0), (H,),
+                      D(w.attr_output_layernorm_gamma), D(w.attr_output_layernorm_beta), 1e-5)
+    inter = F.gelu(x1 @ D(w.inter_kernel) + D(w.inter_bias))
+    want = F.layer_norm(inter @ D(w.output_kernel) + D(w.output_bias) + x1, (H,),
+                        D(w.output_layernorm_gamma), D(w.output_layernorm_beta), 1e-5)
+    torch.testing.assert_close(got.double(), want, rtol=1e-4, atol=1e-4)
