@@ -305,8 +305,15 @@ int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, con
   a.ce.gamma = gamma; a.ce.beta = beta; a.ce.mean = mean; a.ce.var = var;
   a.ce.residual = residual;
   hipStream_t s = (hipStream_t)stream;
-  // every K tile inside one filter tap (and the tap set fits the 64-bit mask): per-tile-tap gather
-  const LaunchFn launch = (C % t.block_k == 0 && KH * KW <= 64) ? in->launch : in->launch_gather;
+  // A loader: the input halo (3x3, stride 1, pad 1, one K tile per tap, no split and the
+  // tile's halo -- its output rows spanned plus a one-row border, W+2 columns, 128 B
+  // per pixel -- within the instance's halo capacity); else the per-tile-tap gather when every K
+  // tile lies inside one tap; else the per-chunk gather
+  const long long halo_rows = (t.block_m - 1) / W + 2 + 2;  // rows a tile can span, plus the border
+  const bool halo = in->launch_halo && KH == 3 && KW == 3 && stride == 1 && dilation == 1 && pad == 1 &&
+                    C == t.block_k && a.splits == 1 && halo_rows * (W + 2) * 128 <= in->halo_bytes;
+  const LaunchFn launch = halo ? in->launch_halo
+                               : (C % t.block_k == 0 && KH * KW <= 64) ? in->launch : in->launch_gather;
   const dim3 grid(a.tiles_m * a.tiles_n * a.splits);  // one workgroup per (tile, K split) item
   if (a.splits > 1) {
     const size_t need = (size_t)split_k * a.M * F * sizeof(float);

@@ -42,7 +42,11 @@ enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
 // A operand loaders: dense rows, the NHWC implicit-GEMM gather for any C
 // (per 16-byte chunk), and the gather for C % BK == 0, where every K tile is one
 // filter tap so the tap decomposition is per tile rather than per chunk.
-enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2 };
+enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2, A_HALO = 3 };
+// LDS bytes of the input halo of a BM-row A_HALO conv tile (see gemm_kernel): the rows
+// BM output pixels can span in an image of width <= 56, plus a one-row border on
+// each side, 58 columns, 128 B per pixel.  Launchers check the actual width fits.
+constexpr int halo_cap(int bm) { return ((bm + 55) / 56 + 3) * 58 * 128; }
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -414,10 +418,22 @@ gemm_kernel(KArgs p) {
   // One LDS array per pipeline stage: distinct objects let the compiler see that
   // the DMA writes into one stage never alias the fragment reads of another, so
   // it does not serialise them with a vmcnt(0) wait.
-  __shared__ __attribute__((aligned(16))) char lds0[G::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char lds1[STAGES > 1 ? G::STAGE_BYTES : 16];
-  __shared__ __attribute__((aligned(16))) char lds2[STAGES > 2 ? G::STAGE_BYTES : 16];
-  __shared__ __attribute__((aligned(16))) char lds3[STAGES > 3 ? G::STAGE_BYTES : 16];
+  // A_HALO (3x3 stride-1 conv, C == BK): the A operand is read from one input
+  // halo per tile -- the tile's output rows plus a one-pixel border, all C
+  // channels -- loaded once before the mainloop; the K tiles are the 9 filter
+  // taps, so the pipeline stages hold B only.
+  constexpr bool HALO = ALOAD == A_HALO;
+  constexpr int HALO_CAP = halo_cap(BM);
+  constexpr int SBYTES = HALO ? G::B_BYTES : G::STAGE_BYTES;  // bytes per stage array
+  constexpr int A_OFF = HALO ? 0 : G::A_BYTES;                // B region offset in a stage
+  constexpr int LA = HALO ? 0 : G::SA;                        // A loads per thread per tile
+  __shared__ __attribute__((aligned(16))) char lds0[SBYTES];
+  __shared__ __attribute__((aligned(16))) char lds1[STAGES > 1 ? SBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char lds2[STAGES > 2 ? SBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char lds3[STAGES > 3 ? SBYTES : 16];
+  __shared__ __attribute__((aligned(16))) char halo_lds[HALO ? HALO_CAP : 16];
+  static_assert(!HALO || (G::ESZ == 2 && BK == 64), "A_HALO: 16-bit data, one 64-channel chunk per pixel");
+  static_assert(!HALO || SBYTES * STAGES + HALO_CAP <= 160 * 1024, "A_HALO: LDS overflow");
   auto stage_base = [&](auto S) -> char ICPP_LDS* ICPP_INLINE {
     constexpr int s = decltype(S)::value;
     if constexpr (s == 0) return (char ICPP_LDS*)lds0;
@@ -492,7 +508,7 @@ gemm_kernel(KArgs p) {
       rb = make_rsrc(Bb + (size_t)col0 * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
     }
 #pragma unroll
-  for (int i = 0; i < NA; ++i) {
+  for (int i = 0; i < (HALO ? 0 : NA); ++i) {
     const int q = tid + i * G::THREADS;
     const int r = q / G::CPR_A;
     const int c = (q % G::CPR_A) ^ G::a_swz(r);
@@ -535,10 +551,63 @@ gemm_kernel(KArgs p) {
     const int c = (q % G::CPR_B) ^ G::b_swz(k);
     b_goff[i] = (uint32_t)(k * p.ldb * ESZ + c * 16);
   }
-  const uint32_t a_row_step = (uint32_t)((G::THREADS / G::CPR_A) * p.lda * ESZ);  // bytes per load (A_UNIFORM)
-  const uint32_t b_row_step = (uint32_t)((G::THREADS / G::CPR_B) * p.ldb * ESZ);  // bytes per load (B_UNIFORM)
   // byte offset of this wave's lane 0 within one load (wave-uniform -> SGPR)
   const int wave_slot = __builtin_amdgcn_readfirstlane(tid >> 6) * 64 * 16;
+  // ---- A_HALO: the tile's input halo in LDS ----------------------------------
+  // Output pixel m = (g, ow) with g = m / W the output row over all images
+  // (stride 1, pad 1, 3x3: OH = H, OW = W).  The tile's rows g0 .. gl need input
+  // rows g0-1 .. gl+1 of the images stacked on top of each other, W+2 columns
+  // (zero border), 64 channels = eight 16-byte chunks per pixel.  Halo pixel q
+  // = (row - (g0 - 1)) * (W + 2) + column keeps chunk c at slot c ^ ((q >> 1) & 7),
+  // so 16 consecutive pixels read by one ds_read_b128 lane group hit distinct
+  // banks.  A tap (kh, kw) of output pixel (g, ow) reads halo pixel
+  // (g - g0 + kh) * (W + 2) + ow + kw; a tap whose input row lies in another
+  // image (oh + kh - 1 outside [0, H)) is masked to zero.
+  constexpr int HL = HALO ? (HALO_CAP / 16 + G::THREADS - 1) / G::THREADS : 1;  // halo loads per thread
+  int h_q[HALO ? G::TM : 1];       // halo pixel of this lane's row of MFMA tile tm at tap (0, 0)
+  int h_vmask[HALO ? G::TM : 1];   // bit kh: tap row kh lies inside the image
+  auto setup_halo = [&](const Item& it) ICPP_INLINE {
+    if constexpr (HALO) {
+      const int Wd = p.cW, Wp = p.cW + 2;
+      const int g0 = it.row0 / Wd;
+#pragma unroll
+      for (int tm = 0; tm < G::TM; ++tm) {
+        int m = it.row0 + wm * G::WTM + tm * MF + (lane % MF);
+        m = min(m, p.M - 1);  // rows past M compute on a valid pixel and are never stored
+        const int g = m / Wd;
+        const int ow = m - g * Wd;
+        const int oh = g % p.cH;
+        h_q[tm] = (g - g0) * Wp + ow;
+        h_vmask[tm] = (oh > 0 ? 1 : 0) | 2 | (oh < p.cH - 1 ? 4 : 0);
+      }
+    }
+  };
+  auto issue_halo = [&](const Item& it) ICPP_INLINE {
+    if constexpr (HALO) {
+      const int Wd = p.cW, Wp = p.cW + 2;
+      const int g0 = it.row0 / Wd;
+      const int gl = (min(it.row0 + BM, p.M) - 1) / Wd;
+      const int nslots = (gl - g0 + 3) * Wp * 8;   // the launcher keeps nslots * 16 <= HALO_CAP
+      const int rows_all = p.M / Wd;               // N * H input rows
+#pragma unroll
+      for (int i = 0; i < HL; ++i) {
+        const int s = i * G::THREADS + tid;
+        if (s < nslots) {
+          const int q = s >> 3;
+          const int hr = q / Wp;
+          const int hc = q - hr * Wp;
+          const int grow = g0 - 1 + hr;
+          const int iw = hc - 1;
+          const int chunk = (s & 7) ^ ((q >> 1) & 7);
+          const bool ok = grow >= 0 && grow < rows_all && iw >= 0 && iw < Wd;
+          const uint32_t off = ok ? (uint32_t)(((grow * Wd + iw) * p.cC + chunk * 8) * ESZ) : p.a_bytes_total;
+          dma16(ra, off, 0u, (char ICPP_LDS*)halo_lds + i * G::THREADS * 16 + wave_slot);
+        }
+      }
+    }
+  };
+  const uint32_t a_row_step = (uint32_t)((G::THREADS / G::CPR_A) * p.lda * ESZ);  // bytes per load (A_UNIFORM)
+  const uint32_t b_row_step = (uint32_t)((G::THREADS / G::CPR_B) * p.ldb * ESZ);  // bytes per load (B_UNIFORM)
 
   // Per-tile part of the A address shared by all loads of the tile starting at
   // K element kk.  For the per-tile-tap gather (C % BK == 0) that tile is filter
@@ -565,8 +634,8 @@ gemm_kernel(KArgs p) {
   auto issue_load = [&](int kk, auto S, auto L, const TileCtx& tc) ICPP_INLINE {
     constexpr int l = decltype(L)::value;
     char ICPP_LDS* as = stage_base(S);
-    char ICPP_LDS* bs = as + G::A_BYTES;
-    if constexpr (l < G::SA) {
+    char ICPP_LDS* bs = as + A_OFF;
+    if constexpr (l < LA) {
       constexpr int i = l;
       if (!(G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS)) return;
       if constexpr (ALOAD == A_DENSE) {
@@ -591,7 +660,7 @@ gemm_kernel(KArgs p) {
         dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
       }
     } else {
-      constexpr int i = l - G::SA;
+      constexpr int i = l - LA;
       if (!(G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS)) return;
       if constexpr (B_UNIFORM)
         dma16(rb, b_goff[0], (uint32_t)(kk * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
@@ -599,7 +668,7 @@ gemm_kernel(KArgs p) {
         dma16(rb, b_goff[i], (uint32_t)(kk * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
     }
   };
-  constexpr int LOADS = G::SA + G::SB;  // loads per thread per tile
+  constexpr int LOADS = LA + G::SB;  // loads per thread per tile
   auto issue_tile = [&](int kk, auto S) ICPP_INLINE {
     const TileCtx tc = tile_ctx(kk);
     static_for<LOADS>([&](auto L) ICPP_INLINE { issue_load(kk, S, L, tc); });
@@ -651,12 +720,23 @@ gemm_kernel(KArgs p) {
     }
   }
 
-  auto load_frags = [&](const char ICPP_LDS* as, const char ICPP_LDS* bs, auto KS, Frag* af, Frag* bf) ICPP_INLINE {
+  auto load_frags = [&](const char ICPP_LDS* as, const char ICPP_LDS* bs, auto KS, Frag* af, Frag* bf,
+                        int tap) ICPP_INLINE {
     constexpr int ks = decltype(KS)::value;
+    // A_HALO: tap (kh, kw) offsets the halo pixel; K chunk of this lane's slice
+    const int t_kh = HALO ? tap / 3 : 0;
+    const int t_off = HALO ? t_kh * (p.cW + 2) + (tap - t_kh * 3) : 0;
+    constexpr int h_chunk = (ks * G::KI) / 8;  // first 16-byte chunk of this K step
 #pragma unroll
     for (int tm = 0; tm < G::TM; ++tm) {
       const uint32_t row_off = (uint32_t)(tm * MF * G::ROWB_A);
-      if constexpr (ESZ == 2) {
+      if constexpr (HALO) {
+        const int q = h_q[tm] + t_off;
+        const int c = (h_chunk + a_kgrp) ^ ((q >> 1) & 7);
+        const i32x4 v = lds_load16((const char ICPP_LDS*)halo_lds, (uint32_t)(q * 128 + c * 16));
+        const bool ok = (h_vmask[tm] >> t_kh) & 1;
+        af[tm] = ok ? v : i32x4{0, 0, 0, 0};
+      } else if constexpr (ESZ == 2) {
         af[tm] = lds_load16(as, a_addr[ks][0] + row_off);
       } else {
         i32x4 lo = lds_load16(as, a_addr[ks][0] + row_off);
@@ -703,12 +783,12 @@ gemm_kernel(KArgs p) {
   // a wave either loads or skips as a whole: per wave the count is LOADS,
   // LOADS-1 or LOADS-2, and vmcnt thresholds follow it.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const int my_loads = (G::A_CHUNKS > 64 * wv ? (G::A_CHUNKS - 64 * wv + G::THREADS - 1) / G::THREADS : 0) +
+  const int my_loads = (!HALO && G::A_CHUNKS > 64 * wv ? (G::A_CHUNKS - 64 * wv + G::THREADS - 1) / G::THREADS : 0) +
                        (G::B_CHUNKS > 64 * wv ? (G::B_CHUNKS - 64 * wv + G::THREADS - 1) / G::THREADS : 0);
   // s_waitcnt vmcnt(TILES * my_loads): at most TILES tiles of this wave's loads still in flight
   auto wait_tiles = [&](auto TILES) ICPP_INLINE {
     constexpr int nt = decltype(TILES)::value;
-    if constexpr (nt == 0 || (G::A_EVEN && G::B_EVEN)) {
+    if constexpr (nt == 0 || ((HALO || G::A_EVEN) && G::B_EVEN)) {
       wait_vmcnt<nt * LOADS>();
     } else {
       if (my_loads == LOADS) wait_vmcnt<nt * LOADS>();
@@ -773,8 +853,9 @@ gemm_kernel(KArgs p) {
       constexpr int CPR_O = G::WTN * OSZ / 16;             // 16-byte chunks per output row
       constexpr int CHUNK_ELEMS = 16 / OSZ;
       constexpr int NQ = (MF * CPR_O + 63) / 64;           // chunks per lane per band
-      constexpr int PER_STAGE = G::STAGE_BYTES / REGION;  // wave regions per stage array
-      static_assert(PER_STAGE * STAGES >= WM * WN, "epilogue staging must fit the LDS stages");
+      // staging space: the pipeline stage arrays, or for A_HALO the halo (free after the mainloop)
+      constexpr int PER_STAGE = (HALO ? HALO_CAP : SBYTES) / REGION;  // wave regions per array
+      static_assert(PER_STAGE * (HALO ? 1 : STAGES) >= WM * WN, "epilogue staging must fit the LDS stages");
       static_assert((G::WTN * OSZ) % 16 == 0, "wave tile rows must be whole 16-byte chunks");
       // store descriptor over this tile's rows (launchers keep BM * ldc * OSZ < 2 GiB)
       const uint64_t rows = (uint64_t)(p.M > row0 ? min(p.M - row0, BM) : 0);
@@ -803,7 +884,8 @@ gemm_kernel(KArgs p) {
         load_band(0);
       }
       const int w_arr = wave / PER_STAGE;
-      char ICPP_LDS* arr = (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
+      char ICPP_LDS* arr = HALO ? (char ICPP_LDS*)halo_lds
+                         : (w_arr == 0) ? (char ICPP_LDS*)lds0 : (w_arr == 1) ? (char ICPP_LDS*)lds1
                          : (w_arr == 2) ? (char ICPP_LDS*)lds2 : (char ICPP_LDS*)lds3;
       char ICPP_LDS* region = arr + (wave % PER_STAGE) * REGION;
       __syncthreads();  // every wave is done reading the pipeline stages
@@ -1000,7 +1082,7 @@ gemm_kernel(KArgs p) {
         // EPI_LN_ROW: the workgroup owns whole rows (tiles_n == 1, N <= BN); two-pass
         // mean / centred variance in registers, cross-wave through LDS.
         __syncthreads();  // mainloop LDS no longer needed
-        static_assert(2 * WN * BM * 4 <= G::STAGE_BYTES, "LN reduction scratch must fit one LDS stage");
+        static_assert(2 * WN * BM * 4 <= SBYTES, "LN reduction scratch must fit one LDS stage");
         float ICPP_LDS* red = (float ICPP_LDS*)lds0;       // [WN][BM]
         float ICPP_LDS* red2 = red + WN * BM;               // [WN][BM]
         const BiasT* gamma = (const BiasT*)p.gamma;
@@ -1077,14 +1159,20 @@ gemm_kernel(KArgs p) {
   auto advance_issue = [&]() ICPP_INLINE { cur_kt = min(cur_kt + 1, nk - 1); };
   auto cur_kk = [&]() ICPP_INLINE { return first.kz * p.k_split + cur_kt * BK; };
 
+  // K tile -> filter tap for A_HALO (C == BK: the K tiles are the taps; clamped for the
+  // prefetch past the last tile, whose fragments are never used)
+  const int kt_base = (first.kz * p.k_split) / BK;
+  auto tap_of = [&](int kt) ICPP_INLINE { return HALO ? min(kt_base + kt, 8) : 0; };
+  setup_halo(first);
+  issue_halo(first);  // older than every B load: landed once tile 0 has
   static_for<STAGES>([&](auto S) ICPP_INLINE {
     if constexpr (decltype(S)::value > 0) advance_issue();
     issue_tile(cur_kk(), S);
   });
   wait_tiles(std::integral_constant<int, STAGES - 1>{});  // this wave's loads of tile 0 landed
   lds_barrier();  // tile 0 published
-  load_frags(stage_base(std::integral_constant<int, 0>{}), stage_base(std::integral_constant<int, 0>{}) + G::A_BYTES,
-             std::integral_constant<int, 0>{}, fa[0], fb[0]);
+  load_frags(stage_base(std::integral_constant<int, 0>{}), stage_base(std::integral_constant<int, 0>{}) + A_OFF,
+             std::integral_constant<int, 0>{}, fa[0], fb[0], tap_of(0));
   for (int kt0 = 0; kt0 < nk; kt0 += STAGES) {
     // the stage index of each step is a compile-time constant: kt0 % STAGES == 0
     static_for<STAGES>([&](auto J) ICPP_INLINE {
@@ -1096,7 +1184,8 @@ gemm_kernel(KArgs p) {
           constexpr int ks = decltype(KS)::value;
           constexpr int s = j * NKS + ks;  // position in the fragment double buffer
           if constexpr (ks + 1 < NKS) {
-            load_frags(as, as + G::A_BYTES, std::integral_constant<int, ks + 1>{}, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            load_frags(as, as + A_OFF, std::integral_constant<int, ks + 1>{}, fa[(s + 1) & 1], fb[(s + 1) & 1],
+                       tap_of(kt));
             mfma_step(fa[s & 1], fb[s & 1]);
             schedule(std::integral_constant<int, 0>{});
           } else {
@@ -1106,7 +1195,8 @@ gemm_kernel(KArgs p) {
             issue_tile(cur_kk(), J);
             constexpr int jn = (j + 1) % STAGES;
             const char ICPP_LDS* an = stage_base(std::integral_constant<int, jn>{});
-            load_frags(an, an + G::A_BYTES, std::integral_constant<int, 0>{}, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            load_frags(an, an + A_OFF, std::integral_constant<int, 0>{}, fa[(s + 1) & 1], fb[(s + 1) & 1],
+                       tap_of(kt + 1));
             mfma_step(fa[s & 1], fb[s & 1]);
             schedule(std::integral_constant<int, LOADS>{});
           }

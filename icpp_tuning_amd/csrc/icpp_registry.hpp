@@ -16,6 +16,8 @@ struct Instance {
   int wave_tile_n;
   LaunchFn launch;         // conv instances: the per-tile-tap gather (C % block_k == 0)
   LaunchFn launch_gather;  // conv instances: the per-chunk gather (any C % 8 == 0); else null
+  LaunchFn launch_halo;    // conv instances: the input-halo loader (3x3 stride 1 pad 1, C == block_k); or null
+  int halo_bytes;          // its halo capacity (halo_cap(block_m))
 };
 
 int register_instance(const Instance& inst);
@@ -52,6 +54,10 @@ Instance make_instance(int family, const char* name) {
   if constexpr (AL == A_IM2COL) {
     in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL_TAP>;
     in.launch_gather = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL>;
+    constexpr bool halo_fits = G::ESZ == 2 && BK == 64 && G::B_BYTES * ST + halo_cap(BM) <= 160 * 1024;
+    if constexpr (halo_fits) in.launch_halo = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_HALO>;
+    else in.launch_halo = nullptr;
+    in.halo_bytes = halo_cap(BM);
   } else {
     in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>;
     in.launch_gather = nullptr;

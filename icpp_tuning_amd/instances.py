@@ -195,6 +195,11 @@ def _conv_tiles() -> List[Inst]:
         _g("f16", 128, 128, 32, 2, 2, 16, st=4, fam=c),
         _g("f16", 64, 128, 64, 1, 4, 16, st=4, fam=c),
         _g("f16", 256, 128, 64, 2, 4, 16, fam=c),
+        # row-aligned / deeper tiles for wide images under the input-halo loader
+        # (224 = 4 rows of 56; 8 waves on 256 rows)
+        _g("f16", 256, 64, 64, 4, 2, 16, fam=c),
+        _g("f16", 224, 64, 64, 2, 2, 16, fam=c),
+        _g("f16", 224, 64, 64, 7, 1, 32, fam=c),
     ]
 
 
