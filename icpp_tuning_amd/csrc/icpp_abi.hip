@@ -107,6 +107,8 @@ int register_instance(const Instance& inst) {
 
 // The row-op translation unit (icpp_rowops.hip) reports through the same buffer.
 int set_last_error(int code, const char* msg) { return fail(code, "%s", msg); }
+int layernorm_rows_f16(const void* X, const void* R, const void* W, const void* B, void* Y, int M, int N, float eps,
+                       hipStream_t s);  // icpp_rowops.hip
 
 }  // namespace icpp
 
@@ -204,6 +206,28 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
                                       const void* residual, const void* gamma, const void* beta, void* Y,
                                       int M, int N, int K, float eps,
                                       void* workspace, size_t ws_bytes, void* stream) {
+  if (family == ICPP_FAMILY_GEMM) {
+    // GEMM-then-LayerNorm: a plain f16 GEMM + bias into Y (staged epilogue, any GEMM tile), then
+    // the row LayerNorm kernel in place (adding the residual); the same HBM traffic as two-pass
+    if (!gamma || !beta) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: null tensor");
+    const Instance* gi = lookup(ICPP_FAMILY_GEMM, inst);
+    if (!gi) return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: no GEMM instance %d", inst);
+    if (gi->tile.dtype != DT_F16) return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: GEMM instance %d is not f16", inst);
+    if (!(eps > 0.f)) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: eps must be > 0");
+    if ((residual && !aligned16(residual)) || !aligned16(gamma) || !aligned16(beta))
+      return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: pointers must be 16-byte aligned");
+    if (residual && M > 0 && N > 0) {
+      // the GEMM writes Y before the LayerNorm reads the residual: they must not share memory
+      const char* r0 = (const char*)residual;
+      const char* y0 = (const char*)Y;
+      const size_t bytes = (size_t)M * N * 2;
+      if (r0 < y0 + bytes && y0 < r0 + bytes)
+        return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: the GEMM family needs a residual that does not overlap Y");
+    }
+    int rc = icpp_gemm(inst, A, B, bias, Y, M, N, K, K, N, N, ICPP_ACT_NONE, 1.f, 1.f, 1, workspace, ws_bytes, stream);
+    if (rc) return rc;
+    return layernorm_rows_f16(Y, residual, gamma, beta, Y, M, N, eps, (hipStream_t)stream);
+  }
   if (family != ICPP_FAMILY_GEMM_LN_ROW && family != ICPP_FAMILY_GEMM_LN_STATS)
     return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: family %d is not a LayerNorm family", family);
   const Instance* in = lookup(family, inst);

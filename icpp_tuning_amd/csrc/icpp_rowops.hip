@@ -97,9 +97,11 @@ __device__ __forceinline__ float row_reduce(float v, Op op, int tpr, float (*red
 // LayerNorm forward: y = (x - mean) * rstd * w + b, mean / rstd (fp32) per row
 // (reference _layer_norm_fwd_fused: centred two-pass variance, rstd = 1/sqrt(var+eps)).
 // ---------------------------------------------------------------------------
+// With a residual R (may be null), x = X + R (R has X's row stride).  Y may be X:
+// every row is held in registers before any of it is written.
 template <typename T, int VEC, int CPT>
 __global__ void __launch_bounds__(1024)
-layernorm_fwd_kernel(const T* __restrict__ X, const T* __restrict__ W, const T* __restrict__ B, T* __restrict__ Y,
+layernorm_fwd_kernel(const T* X, const T* R, const T* __restrict__ W, const T* __restrict__ B, T* Y,
                      float* __restrict__ mean_out, float* __restrict__ rstd_out, int M, int N, int ldx, int ldy,
                      float eps, int tpr) {
   __shared__ float red[2][MAX_WAVES];
@@ -114,8 +116,15 @@ layernorm_fwd_kernel(const T* __restrict__ X, const T* __restrict__ W, const T* 
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = t + i * tpr;
-    if (live && c < nch) load_chunk<T, VEC>(X + (size_t)row * ldx + (size_t)c * VEC, x[i]);
-    else {
+    if (live && c < nch) {
+      load_chunk<T, VEC>(X + (size_t)row * ldx + (size_t)c * VEC, x[i]);
+      if (R != nullptr) {
+        float r[VEC];
+        load_chunk<T, VEC>(R + (size_t)row * ldx + (size_t)c * VEC, r);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[i][e] += r[e];
+      }
+    } else {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) x[i][e] = 0.f;
     }
@@ -411,18 +420,19 @@ hipError_t dispatch_cpt(const RowGeom& g, F&& launch) {
 }
 
 template <typename T>
-int ln_fwd_t(const void* X, const void* W, const void* B, void* Y, float* mean, float* rstd, int M, int N, int ldx,
-             int ldy, float eps, hipStream_t s) {
+int ln_fwd_t(const void* X, const void* R, const void* W, const void* B, void* Y, float* mean, float* rstd, int M,
+             int N, int ldx, int ldy, float eps, hipStream_t s) {
   constexpr int V = 16 / (int)sizeof(T);
   const bool vec_ok = N % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(X) && aligned16(Y) &&
-                      aligned16(W) && aligned16(B);
+                      aligned16(W) && aligned16(B) && (R == nullptr || aligned16(R));
   RowGeom g;
   if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 8 : 16, &g)) return set_error(ICPP_E_SHAPE, "icpp_layernorm_fwd: N too large");
   const int rpb = g.block / g.tpr;
   const dim3 grid((M + rpb - 1) / rpb);
   hipError_t e = dispatch_cpt<T>(g, [&](auto VEC, auto CPT) {
     hipLaunchKernelGGL((layernorm_fwd_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), grid, dim3(g.block), 0, s,
-                       (const T*)X, (const T*)W, (const T*)B, (T*)Y, mean, rstd, M, N, ldx, ldy, eps, g.tpr);
+                       (const T*)X, (const T*)R, (const T*)W, (const T*)B, (T*)Y, mean, rstd, M, N, ldx, ldy, eps,
+                       g.tpr);
     return hipGetLastError();
   });
   return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
@@ -491,6 +501,15 @@ int check_rows(const char* fn, int dtype, int M, int N, int ld_in, int ld_out) {
 
 }  // namespace
 
+namespace icpp {
+// Y = LayerNorm(X [+ R]) * W + B over rows of an f16 [M, N] tensor (row stride N),
+// Y may be X; for icpp_gemm_bias_residual_layernorm's GEMM-then-LayerNorm strategy.
+int layernorm_rows_f16(const void* X, const void* R, const void* W, const void* B, void* Y, int M, int N, float eps,
+                       hipStream_t s) {
+  return ln_fwd_t<_Float16>(X, R, W, B, Y, nullptr, nullptr, M, N, N, N, eps, s);
+}
+}  // namespace icpp
+
 extern "C" {
 
 int icpp_layernorm_fwd(int dtype, const void* X, const void* W, const void* B, void* Y, float* mean, float* rstd,
@@ -499,9 +518,9 @@ int icpp_layernorm_fwd(int dtype, const void* X, const void* W, const void* B, v
   if (int rc = check_rows("icpp_layernorm_fwd: bad dtype or shape", dtype, M, N, ldx, ldy)) return rc;
   if (!(eps >= 0.f)) return set_error(ICPP_E_ARG, "icpp_layernorm_fwd: eps must be >= 0");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == ICPP_F16) return ln_fwd_t<_Float16>(X, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
-  if (dtype == ICPP_BF16) return ln_fwd_t<__bf16>(X, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
-  return ln_fwd_t<float>(X, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
+  if (dtype == ICPP_F16) return ln_fwd_t<_Float16>(X, nullptr, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
+  if (dtype == ICPP_BF16) return ln_fwd_t<__bf16>(X, nullptr, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
+  return ln_fwd_t<float>(X, nullptr, W, B, Y, mean, rstd, M, N, ldx, ldy, eps, s);
 }
 
 size_t icpp_layernorm_bwd_workspace_bytes(int dtype, int M, int N, int ld) {

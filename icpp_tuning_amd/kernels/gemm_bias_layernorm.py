@@ -13,6 +13,9 @@ chosen per shape by the tuner:
   "two_pass"  (gemm_ln_stats)  GEMM tiles write X (f16) into Y and a per-(row,
               wave column block) (mean, M2) pair into the workspace; a finalize
               pass merges the pairs (Chan et al.) and normalises Y in place.
+  "gemm_ln"   (gemm, f16)      a plain GEMM + bias into Y (any GEMM tile, staged
+              stores), then the row LayerNorm kernel in place: the same HBM
+              traffic as two-pass, without the statistics epilogue.
 """
 
 from __future__ import annotations
@@ -27,7 +30,7 @@ from .. import inputs as _inputs
 from .. import runtime
 from ._base import InstanceDescriptor, family_instances, raw_from_inst
 
-STRATEGY_FAMILY = {"row": "gemm_ln_row", "two_pass": "gemm_ln_stats"}
+STRATEGY_FAMILY = {"row": "gemm_ln_row", "two_pass": "gemm_ln_stats", "gemm_ln": "gemm"}
 
 
 class GemmBiasLayerNormDescriptor(InstanceDescriptor):
@@ -48,6 +51,8 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
         fam = self._family(raw)
         mf = int(str(raw["mfma"]).split("x")[0])
         for idx, inst in enumerate(family_instances(fam)):
+            if inst.dtype != self.dtype:
+                continue
             if (inst.bm, inst.bn, inst.bk, inst.stages, inst.threads, inst.wm, inst.wn, inst.mf) == (
                     raw["block_M"], raw["block_N"], raw["block_K"], raw["num_stages"], raw["thread_num"],
                     raw["waves_m"], raw["waves_n"], mf):
@@ -62,7 +67,7 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
         out = []
         for strategy, fam in STRATEGY_FAMILY.items():
             for inst in family_instances(fam):
-                if K % inst.bk:
+                if K % inst.bk or inst.dtype != self.dtype:
                     continue
                 if strategy == "row" and N and (N > inst.bn or inst.bn >= 2 * N):
                     continue  # whole row must fit one tile without wasting half of it
@@ -72,10 +77,10 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
         return out
 
     def format_config(self, raw):
-        return super().format_config(raw) + ("_ROW" if raw.get("strategy") == "row" else "_2P")
+        return super().format_config(raw) + {"row": "_ROW", "gemm_ln": "_GL"}.get(raw.get("strategy"), "_2P")
 
     def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
-        """Two-pass pays one extra read + write of Y at HBM rate (roofline ratio)."""
+        """Two-pass and GEMM-then-LN pay one extra read + write of Y at HBM rate (roofline ratio)."""
         if raw.get("strategy") == "row":
             return base_score
         from ..autotuner.gpu_spec import get_gpu_spec
@@ -101,6 +106,11 @@ def get_gemm_configs(K, N: int = 0):
     return DESCRIPTOR.get_raw_configs(K=K, N=N)
 
 
+def _overlap(a: torch.Tensor, b: torch.Tensor) -> bool:
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    return a0 < b0 + b.numel() * b.element_size() and b0 < a0 + a.numel() * a.element_size()
+
+
 class CompiledGemmLayerNorm:
     def __init__(self, M, N, K, config, eps=1e-5):
         self.M, self.N, self.K, self.config, self.eps = M, N, K, config, eps
@@ -114,6 +124,11 @@ class CompiledGemmLayerNorm:
         need = runtime.workspace_bytes(self.family, self.inst, self.M, self.N, self.K)
         if need and (self._ws is None or self._ws.device != A.device):
             self._ws = runtime.alloc_workspace(need, A.device)
+        if self.family == "gemm" and residual is not None and out is not None and _overlap(out, residual):
+            # GEMM-then-LN writes Y before reading the residual: go through a fresh output
+            y = runtime.gemm_bias_layernorm(self.family, self.inst, A, B, bias, gamma, beta, eps=self.eps,
+                                            workspace=self._ws, residual=residual)
+            return out.copy_(y)
         return runtime.gemm_bias_layernorm(self.family, self.inst, A, B, bias, gamma, beta, out=out,
                                            eps=self.eps, workspace=self._ws, residual=residual)
 

@@ -106,6 +106,10 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
  * (evaluation/end2end.py:76-79, :84-87: matmul + bias, + residual, F.layer_norm).
  * residual is [M, N] f16 (may be Y itself: each element is read before it is
  * written, by the same lane); null gives icpp_gemm_bias_layernorm.
+ * family may also be ICPP_FAMILY_GEMM (an f16 GEMM instance): a plain GEMM + bias
+ * into Y, then the row LayerNorm in place -- the same HBM traffic as the two-pass
+ * family, any GEMM tile.  With that family the residual must not overlap Y
+ * (ICPP_E_ARG otherwise): the GEMM writes Y before the LayerNorm reads it.
  */
 int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
                                       const void* residual, const void* gamma, const void* beta, void* Y,

@@ -82,6 +82,15 @@ def test_validation_errors_before_launch(L):
     assert f(7, 0, 16, 16, None, 16, 16, 16, 64, 64, 64, 1e-5, None, 0, None) == -1
     row = _lib.FAMILY["gemm_ln_row"]
     assert f(row, 0, 16, 16, None, 16, 16, 16, 64, 2048, 64, 1e-5, None, 0, None) == -2  # N > block_n
+    # GEMM-then-LN: f16 GEMM instances only, and the residual may not overlap Y
+    fr = L._dll.icpp_gemm_bias_residual_layernorm
+    gem = _lib.FAMILY["gemm"]
+    gems = family_instances("gemm")
+    i16 = next(i for i, t in enumerate(gems) if t.dtype == "f16")
+    ibf = next(i for i, t in enumerate(gems) if t.dtype == "bf16")
+    assert fr(gem, ibf, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
+    assert fr(gem, i16, 16, 16, None, 4096 + 64, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -4
+    assert "overlap" in L.last_error()
     c = L._dll.icpp_conv2d_nhwc
     assert c(0, 16, 16, 16, 1, 8, 8, 3, 64, 3, 3, 1, 1, 1, 1, None, 0, None) == -2  # C % 8
 
