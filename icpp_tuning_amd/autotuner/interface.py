@@ -52,6 +52,10 @@ class TileLangKernelBase:
     def score_adjustment(self, raw: Dict[str, Any], base_score: float, **shape_kwargs: Any) -> float:
         return base_score
 
+    def schedule_factor(self, raw: Dict[str, Any]) -> float:
+        """Relative mainloop efficiency of the config's schedule (1 for the default one)."""
+        return 1.0
+
     def format_config(self, raw: Dict[str, Any]) -> str:
         """``BM{}_BN{}_BK{}[_SK{}]_S{}_T{}`` (reference :117-128), plus the MFMA
         wave grid / shape suffix when the config carries one."""
@@ -64,6 +68,8 @@ class TileLangKernelBase:
             parts.append(f"W{raw['waves_m']}x{raw['waves_n']}")
         if "mfma" in raw:
             parts.append(f"M{raw['mfma'].split('x')[0]}")
+        if raw.get("sched"):
+            parts.append(str(raw["sched"]).upper())
         return "_".join(parts)
 
     def prune(self, raw_configs: List[Dict[str, Any]], hw: GPUSpec, **shape_kwargs: Any) -> List[Dict[str, Any]]:
@@ -89,7 +95,7 @@ def _score(descriptor: TileLangKernelBase, raw, hw, detailed: bool, shape):
         base = detail["score"]
     else:
         base, detail = score_formula(op, cfg, hw), None
-    return descriptor.score_adjustment(raw, base, **shape), detail
+    return descriptor.score_adjustment(raw, base * descriptor.schedule_factor(raw), **shape), detail
 
 
 def select_best(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None,

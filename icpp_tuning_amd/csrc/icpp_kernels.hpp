@@ -42,7 +42,7 @@ enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
 // A operand loaders: dense rows, the NHWC implicit-GEMM gather for any C
 // (per 16-byte chunk), and the gather for C % BK == 0, where every K tile is one
 // filter tap so the tap decomposition is per tile rather than per chunk.
-enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2, A_HALO = 3 };
+enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2, A_HALO = 3, A_DENSE_PP = 4 };
 // LDS bytes of the input halo of a BM-row A_HALO conv tile (see gemm_kernel): the rows
 // BM output pixels can span in an image of width <= 56, plus a one-row border on
 // each side, 58 columns, 128 B per pixel.  Launchers check the actual width fits.
@@ -423,6 +423,10 @@ gemm_kernel(KArgs p) {
   // channels -- loaded once before the mainloop; the K tiles are the 9 filter
   // taps, so the pipeline stages hold B only.
   constexpr bool HALO = ALOAD == A_HALO;
+  // A_DENSE_PP: dense A with the ping-pong mainloop (two wave groups alternate
+  // between an MFMA phase and a memory phase)
+  constexpr bool DENSE = ALOAD == A_DENSE || ALOAD == A_DENSE_PP;
+  constexpr bool PP = ALOAD == A_DENSE_PP;
   constexpr int HALO_CAP = halo_cap(BM);
   constexpr int SBYTES = HALO ? G::B_BYTES : G::STAGE_BYTES;  // bytes per stage array
   constexpr int A_OFF = HALO ? 0 : G::A_BYTES;                // B region offset in a stage
@@ -480,7 +484,7 @@ gemm_kernel(KArgs p) {
   const char* Ab = (const char*)p.A;
   const char* Bb = (const char*)p.B;
   __amdgpu_buffer_rsrc_t ra, rb;
-  constexpr bool A_UNIFORM = (ALOAD == A_DENSE) && (G::THREADS % G::CPR_A == 0) &&
+  constexpr bool A_UNIFORM = DENSE && (G::THREADS % G::CPR_A == 0) &&
                              ((G::THREADS / G::CPR_A) % (G::RPB_A * G::SWZ_A) == 0);
   constexpr bool B_UNIFORM = (G::THREADS % G::CPR_B == 0) && ((G::THREADS / G::CPR_B) % G::B_SWZ_PERIOD == 0);
   constexpr int NA = A_UNIFORM ? 1 : G::SA;
@@ -497,7 +501,7 @@ gemm_kernel(KArgs p) {
   // for the conv gathers, each lane's input coordinates for its output row.
   auto setup_issue = [&](const Item& it) ICPP_INLINE {
     const int row0 = it.row0, col0 = it.col0;
-    if constexpr (ALOAD == A_DENSE) {
+    if constexpr (DENSE) {
       const uint64_t rem = (uint64_t)(p.M > row0 ? p.M - row0 : 0) * (uint64_t)p.lda * ESZ;
       ra = make_rsrc(Ab + (size_t)row0 * p.lda * ESZ, rem > 0xFFFFFFF0ull ? 0xFFFFFFF0u : (uint32_t)rem);
     } else {
@@ -512,7 +516,7 @@ gemm_kernel(KArgs p) {
     const int q = tid + i * G::THREADS;
     const int r = q / G::CPR_A;
     const int c = (q % G::CPR_A) ^ G::a_swz(r);
-    if constexpr (ALOAD == A_DENSE) {
+    if constexpr (DENSE) {
       a_goff[i] = (uint32_t)(r * p.lda * ESZ + c * G::CH * ESZ);
     } else {
       const int m = row0 + r;
@@ -638,7 +642,7 @@ gemm_kernel(KArgs p) {
     if constexpr (l < LA) {
       constexpr int i = l;
       if (!(G::A_EVEN || tid + i * G::THREADS < G::A_CHUNKS)) return;
-      if constexpr (ALOAD == A_DENSE) {
+      if constexpr (DENSE) {
         if constexpr (A_UNIFORM)
           dma16(ra, a_goff[0], (uint32_t)(kk * ESZ) + i * a_row_step, as + i * G::THREADS * 16 + wave_slot);
         else
@@ -777,7 +781,7 @@ gemm_kernel(KArgs p) {
   // LOADS loads and the vmcnt threshold is a constant.
   constexpr int DS_PER_KS = G::TM * (ESZ == 2 ? 1 : 2) + G::TN * (ESZ == 2 ? 2 : 4);
   constexpr int MFMA_PER_KS = G::TM * G::TN;
-  static_assert((STAGES * NKS) % 2 == 0, "fragment double buffer parity must repeat every STAGES tiles");
+  static_assert(PP || (STAGES * NKS) % 2 == 0, "fragment double buffer parity must repeat every STAGES tiles");
   // Loads this wave issues per tile.  Tile loads cover whole waves (chunk
   // counts are multiples of 64), so in the last, partial round of A or B loads
   // a wave either loads or skips as a whole: per wave the count is LOADS,
@@ -951,9 +955,9 @@ gemm_kernel(KArgs p) {
               if (m < p.M && n < p.N) Vec4Store<float>::st(ws + (size_t)m * p.N + n, get4(tm, tn, g));
             }
         }
-      } else if (ALOAD != A_DENSE && p.ce.flags != 0) {
+      } else if (!DENSE && p.ce.flags != 0) {
         // fused conv epilogue (reference conv2d_bn / conv2d_bn_relu / conv_bn_add_relu)
-        if constexpr (ALOAD != A_DENSE) {
+        if constexpr (!DENSE) {
           f32x4 sc[G::TN][NG], sh[G::TN][NG];
 #pragma unroll
           for (int tn = 0; tn < G::TN; ++tn)
@@ -1163,6 +1167,120 @@ gemm_kernel(KArgs p) {
   // prefetch past the last tile, whose fragments are never used)
   const int kt_base = (first.kz * p.k_split) / BK;
   auto tap_of = [&](int kt) ICPP_INLINE { return HALO ? min(kt_base + kt, 8) : 0; };
+  if constexpr (PP) {
+    // ---- ping-pong mainloop ----------------------------------------------------
+    // Waves w and w + 4 share a SIMD, and group g = wm holds one wave per SIMD.
+    // Every phase ends with one workgroup barrier.  In phase 2j group 0 reads the
+    // fragments of tile j (memory phase) while group 1 multiplies tile j-1 (MFMA
+    // phase); in phase 2j+1 group 0 multiplies tile j while group 1 reads it.  On
+    // each SIMD one wave streams MFMAs from registers while the other fetches, so
+    // the two no longer split the matrix core and then wait for each other at the
+    // tile barrier.
+    // Tile loads, S = STAGES: in phase 2j every wave issues its share of tile
+    // j+S-1 into stage (j-1) % S (its previous tile, j-1, was read in phases 2j-2
+    // and 2j-1), and at the end of phase 2j+1 waits until at most S-2 of its
+    // tiles are in flight -- tile j+1 has landed -- so the barrier ending phase
+    // 2j+1 publishes it.  Barriers per wave: 2 nk (phases 0 .. 2nk-1); group 1's
+    // last MFMA phase (2nk) has none and runs while group 0 reaches the epilogue.
+    static_assert(WM == 2 && WN == 4 && STAGES >= 2 && EPI == EPI_STORE,
+                  "ping-pong: 2 x 4 waves (one wave of each group per SIMD), store epilogue");
+    // The fragments of one tile live from its memory phase to its MFMA phase of
+    // the same iteration only; the accumulators are the only loop-carried state.
+    auto read_tile = [&](auto J, Frag (&fa_)[NKS][G::TM], Frag (&fb_)[NKS][G::TN]) ICPP_INLINE {
+      const char ICPP_LDS* as = stage_base(J);
+      static_for<NKS>([&](auto KS) ICPP_INLINE {
+        constexpr int ks = decltype(KS)::value;
+        load_frags(as, as + A_OFF, KS, fa_[ks], fb_[ks], 0);
+      });
+    };
+    auto mfma_tile = [&](Frag (&fa_)[NKS][G::TM], Frag (&fb_)[NKS][G::TN]) ICPP_INLINE {
+      static_for<NKS>([&](auto KS) ICPP_INLINE {
+        constexpr int ks = decltype(KS)::value;
+        mfma_step(fa_[ks], fb_[ks]);
+      });
+    };
+    auto phase_end = [&]() ICPP_INLINE {
+      __builtin_amdgcn_sched_barrier(0);
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // memory phase: the tile loads spread over the fragment reads
+    auto sched_mem = [&]() ICPP_INLINE {
+      constexpr int DS = NKS * DS_PER_KS;
+      static_for<LOADS>([&](auto I) ICPP_INLINE {
+        constexpr int i = decltype(I)::value;
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        constexpr int ds = (i + 1) * DS / LOADS - i * DS / LOADS;
+        if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);
+      });
+    };
+    // MFMA phase: NL tile loads spread over the MFMAs
+    auto sched_mfma = [&](auto NL) ICPP_INLINE {
+      constexpr int nl = decltype(NL)::value;
+      constexpr int NM = NKS * MFMA_PER_KS;
+      static_for<NM>([&](auto I) ICPP_INLINE {
+        constexpr int i = decltype(I)::value;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        constexpr int l = (i + 1) * nl / NM - i * nl / NM;
+        if constexpr (l > 0) __builtin_amdgcn_sched_group_barrier(0x020, l, 0);
+      });
+    };
+    // K element of tile t; past the last tile the fetch is clamped to it (a cached
+    // re-read into a stage nobody reads again), so every even phase issues LOADS loads
+    const int kbase = first.kz * p.k_split;
+    auto tile_k = [&](int t) ICPP_INLINE { return kbase + min(t, nk - 1) * BK; };
+    constexpr int S = STAGES;
+    static_for<S - 1>([&](auto I) ICPP_INLINE { issue_tile(tile_k(decltype(I)::value), I); });
+    wait_tiles(std::integral_constant<int, S - 2>{});  // this wave's loads of tile 0 landed
+    lds_barrier();                                     // tile 0 published
+    if (__builtin_amdgcn_readfirstlane(wm) == 0) {
+      for (int kt0 = 0; kt0 < nk; kt0 += S) {
+        static_for<S>([&](auto J) ICPP_INLINE {
+          constexpr int j = decltype(J)::value;
+          const int kt = kt0 + j;
+          if (kt < nk) {
+            Frag fa_[NKS][G::TM], fb_[NKS][G::TN];
+            // phase 2kt: issue tile kt+S-1, read tile kt
+            issue_tile(tile_k(kt + S - 1), std::integral_constant<int, (j + S - 1) % S>{});
+            read_tile(J, fa_, fb_);
+            sched_mem();
+            phase_end();
+            // phase 2kt+1: multiply tile kt; then this wave's loads of tile kt+1 have landed
+            mfma_tile(fa_, fb_);
+            sched_mfma(std::integral_constant<int, 0>{});
+            // a scheduling fence keeps the wait behind the MFMAs (left free, the
+            // scheduler hoists it to the start of the phase and the MFMAs stall on
+            // the loads just issued)
+            __builtin_amdgcn_sched_barrier(0);
+            wait_tiles(std::integral_constant<int, S - 2>{});
+            phase_end();
+          }
+        });
+      }
+    } else {
+      issue_tile(tile_k(S - 1), std::integral_constant<int, S - 1>{});
+      phase_end();  // phase 0: group 1 has nothing to multiply yet
+      for (int kt0 = 0; kt0 < nk; kt0 += S) {
+        static_for<S>([&](auto J) ICPP_INLINE {
+          constexpr int j = decltype(J)::value;
+          const int kt = kt0 + j;
+          if (kt < nk) {
+            Frag fa_[NKS][G::TM], fb_[NKS][G::TN];
+            // phase 2kt+1: read tile kt; this wave's loads of tile kt+1 have landed
+            read_tile(J, fa_, fb_);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_tiles(std::integral_constant<int, S - 2>{});
+            phase_end();
+            // phase 2kt+2: multiply tile kt; issue tile kt+S into the stage tile kt leaves
+            issue_tile(tile_k(kt + S), J);
+            mfma_tile(fa_, fb_);
+            sched_mfma(std::integral_constant<int, LOADS>{});
+            if (kt + 1 < nk) phase_end();
+          }
+        });
+      }
+    }
+  } else {
   setup_halo(first);
   issue_halo(first);  // older than every B load: landed once tile 0 has
   static_for<STAGES>([&](auto S) ICPP_INLINE {
@@ -1203,6 +1321,7 @@ gemm_kernel(KArgs p) {
         });
       }
     });
+  }
   }
   wait_vmcnt<0>();  // no LDS-DMA write may land after this point (epilogue staging, next workgroup)
   epilogue(first);

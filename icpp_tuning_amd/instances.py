@@ -13,6 +13,14 @@ Families
   gemm_ln_stats GEMM+bias writing X plus per-(row, wave column block) LN stats
   gemm_ln_row   GEMM+bias+LayerNorm, one workgroup owns whole rows (N <= BN)
   conv2d        NHWC implicit GEMM (A gathered per 16-byte channel chunk)
+
+Mainloop schedules (``sched``)
+  ""            every wave streams MFMAs and its fragment reads together; one
+                workgroup barrier per K tile
+  "pp"          ping-pong (2 x 4 waves, gemm family): the wave group of each row
+                half alternates between an MFMA-only phase and a memory phase
+                (fragment reads + tile loads), offset by one phase from the other
+                group, so the two waves of a SIMD never split its matrix core
 """
 
 from __future__ import annotations
@@ -39,11 +47,12 @@ class Inst:
     wn: int
     mf: int
     stages: int
+    sched: str = ""
 
     @property
     def name(self) -> str:
         return (f"{self.family}_{self.dtype}_{self.bm}x{self.bn}x{self.bk}"
-                f"_w{self.wm}x{self.wn}_m{self.mf}_s{self.stages}")
+                f"_w{self.wm}x{self.wn}_m{self.mf}_s{self.stages}" + (f"_{self.sched}" if self.sched else ""))
 
     @property
     def threads(self) -> int:
@@ -93,12 +102,26 @@ class Inst:
         loads = -(-(self.bm * self.bk * e // 16) // self.threads) - (-(self.bk * self.bn * e // 16) // self.threads)
         if loads * (self.stages - 1) >= 64:
             problems.append("too many loads in flight for vmcnt")
+        if self.sched not in ("", "pp"):
+            problems.append("unknown mainloop schedule")
+        if self.sched == "pp" and (self.family != "gemm" or (self.wm, self.wn) != (2, 4)):
+            problems.append("ping-pong needs the gemm family and a 2 x 4 wave grid")
         if problems:
             raise ValueError(f"{self.name}: " + "; ".join(problems))
 
 
 def _g(dtype, bm, bn, bk, wm, wn, mf, st=2, fam="gemm"):
     return Inst(fam, dtype, bm, bn, bk, wm, wn, mf, st)
+
+
+def _with_pp(tiles: List[Inst]) -> List[Inst]:
+    """Each 2 x 4-wave tile plus its ping-pong twin."""
+    out = []
+    for t in tiles:
+        out.append(t)
+        if (t.wm, t.wn) == (2, 4):
+            out.append(Inst(t.family, t.dtype, t.bm, t.bn, t.bk, t.wm, t.wn, t.mf, t.stages, "pp"))
+    return out
 
 
 # 4-wave 256x256 tiles (128x128 per wave) are left out: 256 accumulator
@@ -203,7 +226,7 @@ def _conv_tiles() -> List[Inst]:
     ]
 
 
-INSTANCES: List[Inst] = (_gemm_tiles("f16") + _gemm_tiles("bf16") + _fp8_tiles()
+INSTANCES: List[Inst] = (_with_pp(_gemm_tiles("f16")) + _with_pp(_gemm_tiles("bf16")) + _with_pp(_fp8_tiles())
                          + _ln_tiles() + _conv_tiles())
 
 for _i in INSTANCES:

@@ -32,6 +32,8 @@ def raw_from_inst(inst: Inst, split_k: Optional[int] = None) -> Dict[str, Any]:
     }
     if split_k is not None:
         raw["split_k"] = split_k
+    if inst.sched:
+        raw["sched"] = inst.sched
     return raw
 
 
@@ -61,6 +63,8 @@ class InstanceDescriptor(TileLangKernelBase):
             if "waves_m" in raw and (inst.wm, inst.wn) != (raw["waves_m"], raw["waves_n"]):
                 continue
             if mf is not None and inst.mf != mf:
+                continue
+            if inst.sched != raw.get("sched", ""):
                 continue
             return idx
         raise KeyError(f"{self.name}: no compiled {self.family}/{self.dtype} instance for {self.format_config(raw)}")
@@ -104,6 +108,11 @@ class InstanceDescriptor(TileLangKernelBase):
             num_stages=raw["num_stages"], num_warps=raw["thread_num"] // 64, warp_size=64,
             a_bytes=e, b_bytes=e, mfma=raw.get("mfma", ""), waves_m=raw.get("waves_m", 0),
             waves_n=raw.get("waves_n", 0), split_k=raw.get("split_k", 1), vgprs=vgprs)
+
+    def schedule_factor(self, raw: Dict[str, Any]) -> float:
+        """The ping-pong mainloop measured 2-8% faster than its default-schedule twin
+        on 4096^3 - 8192^3 bf16 (same tile, bit-identical results)."""
+        return 1.03 if raw.get("sched") == "pp" else 1.0
 
     def gemm_mn(self, **shape) -> tuple:
         return shape["M"], shape["N"]

@@ -51,7 +51,7 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
         fam = self._family(raw)
         mf = int(str(raw["mfma"]).split("x")[0])
         for idx, inst in enumerate(family_instances(fam)):
-            if inst.dtype != self.dtype:
+            if inst.dtype != self.dtype or inst.sched != raw.get("sched", ""):
                 continue
             if (inst.bm, inst.bn, inst.bk, inst.stages, inst.threads, inst.wm, inst.wn, inst.mf) == (
                     raw["block_M"], raw["block_N"], raw["block_K"], raw["num_stages"], raw["thread_num"],
