@@ -407,6 +407,33 @@ struct Tile {
   }
 };
 
+// One split-K output group: C[m, n..n+3] = epilogue(sum_z ws[z][m][n..n+3]), the
+// partials summed in slice order.  With ce.flags set (conv instances) the fused
+// conv epilogue replaces bias/alpha.
+template <int DT>
+__device__ __forceinline__ void splitk_group(const float* ws, void* C, const void* bias, int M, int N, int ldc,
+                                             int splits, float alpha, int act, const ConvEpiArgs& ce, int m, int n) {
+  typedef typename DTraits<DT>::OutT OutT;
+  typedef typename DTraits<DT>::BiasT BiasT;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < splits; ++z) s += Vec4Store<float>::ld(ws + ((size_t)z * M + m) * N + n);
+  if (ce.flags != 0) {
+    f32x4 sc, sh;
+    conv_bn4<BiasT>(ce, N, n, sc, sh);
+    f32x4 r = {0.f, 0.f, 0.f, 0.f};
+    if (ce.flags & CEPI_RESIDUAL) r = Vec4Store<OutT>::ld((const OutT*)ce.residual + (size_t)m * ldc + n);
+    dispatch_relu(act, [&](auto ACT) { s = conv_epi4<decltype(ACT)::value, OutT>(s, sc, sh, r); });
+  } else {
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr) bv = Vec4Store<BiasT>::ld((const BiasT*)bias + n);
+    dispatch_act(act, [&](auto ACT) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = act_fn<decltype(ACT)::value>(s[e] * alpha + bv[e]);
+    });
+  }
+  Vec4Store<OutT>::st((OutT*)C + (size_t)m * ldc + n, s);
+}
+
 // ---------------------------------------------------------------------------
 // The mainloop + epilogue kernel
 // ---------------------------------------------------------------------------
@@ -1358,31 +1385,10 @@ template <int DT>
 __global__ void __launch_bounds__(256)
 splitk_reduce_kernel(const float* __restrict__ ws, void* C, const void* bias, int M, int N, int ldc,
                      int splits, float alpha, int act, ConvEpiArgs ce) {
-  typedef typename DTraits<DT>::OutT OutT;
-  typedef typename DTraits<DT>::BiasT BiasT;
   const size_t groups = (size_t)M * (N / 4);
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < groups; gi += stride) {
-    const int m = (int)(gi / (N / 4));
-    const int n = (int)(gi % (N / 4)) * 4;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int z = 0; z < splits; ++z) s += Vec4Store<float>::ld(ws + ((size_t)z * M + m) * N + n);
-    if (ce.flags != 0) {
-      f32x4 sc, sh;
-      conv_bn4<BiasT>(ce, N, n, sc, sh);
-      f32x4 r = {0.f, 0.f, 0.f, 0.f};
-      if (ce.flags & CEPI_RESIDUAL) r = Vec4Store<OutT>::ld((const OutT*)ce.residual + (size_t)m * ldc + n);
-      dispatch_relu(act, [&](auto ACT) { s = conv_epi4<decltype(ACT)::value, OutT>(s, sc, sh, r); });
-    } else {
-      f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-      if (bias != nullptr) bv = Vec4Store<BiasT>::ld((const BiasT*)bias + n);
-      dispatch_act(act, [&](auto ACT) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[e] = act_fn<decltype(ACT)::value>(s[e] * alpha + bv[e]);
-      });
-    }
-    Vec4Store<OutT>::st((OutT*)C + (size_t)m * ldc + n, s);
-  }
+  for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < groups; gi += stride)
+    splitk_group<DT>(ws, C, bias, M, N, ldc, splits, alpha, act, ce, (int)(gi / (N / 4)), (int)(gi % (N / 4)) * 4);
 }
 
 // ---------------------------------------------------------------------------
