@@ -383,8 +383,11 @@ struct Tile {
   // +8 (b16, 16x16) / +32 (b8, 16x16).  The chosen bits of k separate all of
   // them into distinct bank slots; only bits that are constant per lane over
   // the K steps are used, so addresses stay base + immediate.
+  // Rows of 256·n bytes take the wide pattern; other lengths (128 B, or 384 B for
+  // 192-column f16 tiles, which repeat the 128-B bank pattern since 384 = 128 mod
+  // 256) the narrow one, whose XOR stays inside each group of 8 chunks.
   static __device__ __forceinline__ int b_swz(int k) {
-    constexpr bool WIDE = ROWB_B >= 256;
+    constexpr bool WIDE = ROWB_B % 256 == 0;
     if constexpr (ESZ == 2) {
       if constexpr (MF == 16)
         return WIDE ? (((k & 3) << 1) | (((k >> 3) & 1) << 3)) : ((((k >> 1) & 1) << 1) | (((k >> 3) & 1) << 2));

@@ -152,6 +152,10 @@ def _gemm_tiles(dtype: str) -> List[Inst]:
         _g(dtype, 64, 64, 64, 2, 2, 16, st=4),
         _g(dtype, 32, 128, 64, 1, 4, 16, st=4),
         _g(dtype, 16, 128, 64, 1, 4, 16, st=4),
+        # 192-column tiles: 8192 x 768 outputs in exactly 256 tiles (one per CU)
+        _g(dtype, 128, 192, 64, 2, 2, 16),
+        _g(dtype, 128, 192, 64, 2, 2, 16, st=3),
+        _g(dtype, 128, 192, 64, 2, 4, 16),
     ]
 
 
