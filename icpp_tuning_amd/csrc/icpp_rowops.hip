@@ -227,9 +227,158 @@ softmax_kernel(const T* __restrict__ X, T* __restrict__ Y, int M, int N, int ldx
 // fp32 and written as one partial row per workgroup: part[g][0..N) = dw,
 // part[g][N..2N) = db.
 // ---------------------------------------------------------------------------
+// One row chunk as stored: 16 bytes (VEC elements), or a single element.
+template <typename T, int VEC>
+struct Chunk {
+  typedef i32x4 raw;
+  static __device__ __forceinline__ raw load(const T* p) { return *reinterpret_cast<const i32x4*>(p); }
+  static __device__ __forceinline__ raw zero() { return i32x4{0, 0, 0, 0}; }
+  static __device__ __forceinline__ void unpack(const raw& r, float* out) {
+    T e[VEC];
+    __builtin_memcpy(e, &r, 16);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) out[i] = to_f(e[i]);
+  }
+};
+template <typename T>
+struct Chunk<T, 1> {
+  typedef T raw;
+  static __device__ __forceinline__ raw load(const T* p) { return *p; }
+  static __device__ __forceinline__ raw zero() { return from_f<T>(0.f); }
+  static __device__ __forceinline__ void unpack(const raw& r, float* out) { out[0] = to_f(r); }
+};
+
 template <typename T, int VEC, int CPT>
 __global__ void __launch_bounds__(BWD_BLOCK)
 layernorm_bwd_kernel(const T* __restrict__ DY, const T* __restrict__ X, const T* __restrict__ W,
+                     const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ DX,
+                     float* __restrict__ part, int M, int N, int ld, int tpr) {
+  typedef Chunk<T, VEC> Ch;
+  typedef typename Ch::raw Raw;
+  __shared__ float red[2][MAX_WAVES];
+  __shared__ f32x4 fold[BWD_BLOCK];  // row-slot folding, one 16-byte value per thread
+  int slot = 0;
+  const int rpb = blockDim.x / tpr;
+  const int rs = threadIdx.x / tpr;  // row slot within the workgroup
+  const int t = threadIdx.x % tpr;
+  const int nch = (N + VEC - 1) / VEC;
+  const float inv_n = 1.f / (float)N;
+  // x, dy and w stay in their storage type (half the registers of fp32 copies for
+  // 16-bit data), so the next rows' chunks can be in flight while this row reduces
+  Raw wr[CPT];
+  float dw[CPT][VEC], db[CPT][VEC];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = t + i * tpr;
+    wr[i] = c < nch ? Ch::load(W + (size_t)c * VEC) : Ch::zero();
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      dw[i][e] = 0.f;
+      db[i][e] = 0.f;
+    }
+  }
+  static_assert((int)sizeof(T) * VEC * CPT <= 16, "prefetching backward: at most 16 bytes of a row per thread");
+  Raw nx[CPT], ndy[CPT];
+  float nmean = 0.f, nrstd = 0.f;
+  auto fetch = [&](int row) {
+    const bool live = row < M;
+    nmean = live ? mean_in[row] : 0.f;
+    nrstd = live ? rstd_in[row] : 0.f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = t + i * tpr;
+      const bool ok = live && c < nch;
+      nx[i] = ok ? Ch::load(X + (size_t)row * ld + (size_t)c * VEC) : Ch::zero();
+      ndy[i] = ok ? Ch::load(DY + (size_t)row * ld + (size_t)c * VEC) : Ch::zero();
+    }
+  };
+  // rows rs + rpb * (blockIdx.x + k * gridDim.x): every thread runs the same trip count
+  const int stride = rpb * gridDim.x;
+  fetch(blockIdx.x * rpb + rs);
+  for (int base = blockIdx.x * rpb; base < M; base += stride) {
+    const int row = base + rs;
+    const bool live = row < M;
+    Raw cx[CPT], cdy[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      cx[i] = nx[i];
+      cdy[i] = ndy[i];
+    }
+    const float mean = nmean, rstd = nrstd;
+    if (base + stride < M) fetch(base + stride + rs);  // the next rows load during this row's reductions
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = t + i * tpr;
+      float xv[VEC], dyv[VEC], w[VEC];
+      Ch::unpack(cx[i], xv);
+      Ch::unpack(cdy[i], dyv);
+      Ch::unpack(wr[i], w);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float xh = (live && c < nch) ? (xv[e] - mean) * rstd : 0.f;
+        const float wdy = w[e] * dyv[e];
+        s1 += xh * wdy;
+        s2 += wdy;
+      }
+    }
+    const float c1 = row_reduce(s1, Sum{}, tpr, red, slot) * inv_n;
+    const float c2 = row_reduce(s2, Sum{}, tpr, red, slot) * inv_n;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = t + i * tpr;
+        if (c < nch) {
+          float xv[VEC], dyv[VEC], w[VEC], dx[VEC];
+          Ch::unpack(cx[i], xv);
+          Ch::unpack(cdy[i], dyv);
+          Ch::unpack(wr[i], w);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float xh = (xv[e] - mean) * rstd;
+            const float wdy = w[e] * dyv[e];
+            dx[e] = (wdy - (xh * c1 + c2)) * rstd;
+            dw[i][e] += dyv[e] * xh;
+            db[i][e] += dyv[e];
+          }
+          store_chunk<T, VEC>(DX + (size_t)row * ld + (size_t)c * VEC, dx);
+        }
+      }
+    }
+  }
+  // fold the row slots into slot 0 (fixed order: slot 0 + 1 + 2 + ...), 4 floats at a time
+  float* out = part + (size_t)blockIdx.x * 2 * N;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+#pragma unroll
+      for (int e0 = 0; e0 < VEC; e0 += 4) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (e0 + e < VEC) ? (which ? db[i][e0 + e] : dw[i][e0 + e]) : 0.f;
+        __syncthreads();  // previous round's reads are done
+        fold[threadIdx.x] = v;
+        __syncthreads();
+        if (rs == 0) {
+          for (int r = 1; r < rpb; ++r) v += fold[r * tpr + t];
+          const int c = t + i * tpr;
+          if (c < nch) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (e0 + e < VEC) out[(size_t)which * N + (size_t)c * VEC + e0 + e] = v[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Rows longer than one 16-byte chunk per thread (2 chunks, N <= 16384 for 16-bit
+// types): x, dy, xhat and w*dy of the row in fp32 registers, no prefetch.
+template <typename T, int VEC, int CPT>
+__global__ void __launch_bounds__(BWD_BLOCK)
+layernorm_bwd_kernel_long(const T* __restrict__ DY, const T* __restrict__ X, const T* __restrict__ W,
                      const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ DX,
                      float* __restrict__ part, int M, int N, int ld, int tpr) {
   __shared__ float red[2][MAX_WAVES];
@@ -454,13 +603,15 @@ int softmax_t(const void* X, void* Y, int M, int N, int ldx, int ldy, hipStream_
   return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
 }
 
-// Backward geometry: w, dw, db and the row's x / dy / xhat / w*dy stay in
-// registers, and a 1024-thread workgroup leaves each wave 128 VGPRs: at most 2
-// chunks per thread (16 elements of a 16-bit type; N <= 16384) or 4 scalar ones.
+// Backward geometry: w, dw, db and the row's x / dy stay in registers, and a
+// 1024-thread workgroup leaves each wave 128 VGPRs.  One 16-byte chunk per
+// thread (up to 1024 threads per row: N <= 8192 for 16-bit types) leaves room to
+// prefetch the next rows; longer rows take 2 chunks per thread (N <= 16384)
+// without the prefetch.  The scalar path holds at most 4 elements per thread.
 bool bwd_geom(int dtype, int N, int ld, bool ptrs_aligned, RowGeom* g) {
   const int V = 16 / esize(dtype);
   const bool vec_ok = N % V == 0 && ld % V == 0 && ptrs_aligned;
-  if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 2 : 4, g)) return false;
+  if (vec_ok ? !row_geom(N, V, 1, g) && !row_geom(N, V, 2, g) : !row_geom(N, 1, 4, g)) return false;
   g->block = BWD_BLOCK;
   return true;
 }
@@ -479,8 +630,13 @@ int ln_bwd_t(const void* DY, const void* X, const void* W, const float* mean, co
     if constexpr (decltype(CPT)::value > 4 || (decltype(VEC)::value > 1 && decltype(CPT)::value > 2)) {
       return hipErrorInvalidValue;  // outside the backward's register budget (row_geom never picks it)
     } else {
-      hipLaunchKernelGGL((layernorm_bwd_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), dim3(G), dim3(g.block),
-                         0, s, (const T*)DY, (const T*)X, (const T*)W, mean, rstd, (T*)DX, part, M, N, ld, g.tpr);
+      constexpr int V = decltype(VEC)::value, C = decltype(CPT)::value;
+      if constexpr ((int)sizeof(T) * V * C <= 16)
+        hipLaunchKernelGGL((layernorm_bwd_kernel<T, V, C>), dim3(G), dim3(g.block), 0, s, (const T*)DY, (const T*)X,
+                           (const T*)W, mean, rstd, (T*)DX, part, M, N, ld, g.tpr);
+      else
+        hipLaunchKernelGGL((layernorm_bwd_kernel_long<T, V, C>), dim3(G), dim3(g.block), 0, s, (const T*)DY,
+                           (const T*)X, (const T*)W, mean, rstd, (T*)DX, part, M, N, ld, g.tpr);
       return hipGetLastError();
     }
   });

@@ -134,9 +134,12 @@ def test_rowops_validation_errors_before_launch(L):
     assert sm(f32, None, 16, 4, 64, 64, 64, None) == -4
     assert sm(f32, 16, 16, 4, 20000, 20001, 20001, None) == -2                        # scalar path limit 16384
     ws = L.layernorm_bwd_workspace_bytes
-    # N = 8192 f16: 512 threads per row, 2 rows per 1024-thread workgroup
+    # N = 8192 f16: one 16-byte chunk per thread, 1024 threads = one row per workgroup
     assert ws(f16, 4096, 8192, 8192) == 256 * 2 * 8192 * 4
-    assert ws(f16, 100, 8192, 8192) == 50 * 2 * 8192 * 4
+    assert ws(f16, 100, 8192, 8192) == 100 * 2 * 8192 * 4
+    # N = 1024 f16: the larger of the vector geometry (128 threads per row, 8 rows per
+    # workgroup: 13 groups) and the scalar one (256 threads per row, 4 rows: 25 groups)
+    assert ws(f16, 100, 1024, 1024) == 25 * 2 * 1024 * 4
     assert ws(f16, 4096, 32768, 32768) == 0                                           # beyond the backward's limit
     args = (f16, 16, 16, 16, 16, 16, 16, 16, 16, 4096, 8192, 8192)
     assert bwd(*args, None, 0, None) == -3                                             # no workspace
