@@ -72,19 +72,40 @@ class BertLayerWeights:
 
 
 def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch.Tensor,
-                   softmax=runtime.softmax) -> torch.Tensor:
-    """softmax(q k^T / sqrt(d) + mask) v over heads, [b, s, 3H] -> [b, s, H] (end2end.py:47-71).
-    The batched products run in torch (with contiguous operands); the softmax is icpp_softmax
-    unless another row softmax is given."""
+                   softmax=None, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(q k^T / sqrt(d) + mask) v over heads, [b, s, 3H] -> [b, s, H] (end2end.py:47-71),
+    with q, k, v taken from qkv (+ bias, [3H], when given).
+
+    Default path: one strided add writes (qkv + bias) head-major as [3, b, h, s, d], the
+    scores come from one batched product, and icpp_softmax_scaled_masked applies the scale,
+    the additive mask and the softmax in one pass.  With ``softmax`` given (a row softmax),
+    the reference's order is kept op for op -- scale, mask add, softmax -- as the torch
+    composition this layer is measured against."""
     b, s, _ = qkv.shape
     H = head_num * head_size
-    q1, k1, v1 = qkv.chunk(3, dim=-1)
-    q = transpose_for_scores(q1, head_num, head_size).permute(0, 2, 1, 3).reshape(b * head_num, s, head_size).contiguous()
-    k = transpose_for_scores(k1, head_num, head_size).permute(0, 2, 3, 1).reshape(b * head_num, head_size, s).contiguous()
-    v = transpose_for_scores(v1, head_num, head_size).permute(0, 2, 1, 3).reshape(b * head_num, s, head_size).contiguous()
-    scores = torch.bmm(q, k) * (1.0 / math.sqrt(head_size))
-    scores = (scores.view(b, head_num, s, s) + mask).reshape(b * head_num * s, s)
-    attn = softmax(scores.contiguous()).view(b * head_num, s, s)
+    if softmax is not None:
+        if bias is not None:
+            qkv = qkv + bias
+        q1, k1, v1 = qkv.chunk(3, dim=-1)
+        q = transpose_for_scores(q1, head_num, head_size).permute(0, 2, 1, 3).reshape(b * head_num, s, head_size).contiguous()
+        k = transpose_for_scores(k1, head_num, head_size).permute(0, 2, 3, 1).reshape(b * head_num, head_size, s).contiguous()
+        v = transpose_for_scores(v1, head_num, head_size).permute(0, 2, 1, 3).reshape(b * head_num, s, head_size).contiguous()
+        scores = torch.bmm(q, k) * (1.0 / math.sqrt(head_size))
+        scores = (scores.view(b, head_num, s, s) + mask).reshape(b * head_num * s, s)
+        attn = softmax(scores.contiguous()).view(b * head_num, s, s)
+    else:
+        heads = qkv.view(b, s, 3, head_num, head_size).permute(2, 0, 3, 1, 4)   # [3, b, h, s, d] view
+        t = torch.empty((3, b, head_num, s, head_size), dtype=qkv.dtype, device=qkv.device)
+        if bias is not None:
+            torch.add(heads, bias.view(3, 1, head_num, 1, head_size), out=t)
+        else:
+            t.copy_(heads)
+        q = t[0].view(b * head_num, s, head_size)
+        v = t[2].view(b * head_num, s, head_size)
+        k = t[1].view(b * head_num, s, head_size).transpose(1, 2).contiguous()    # [b*h, d, s]
+        scores = torch.bmm(q, k).view(b * head_num * s, s)
+        attn = runtime.softmax_scaled_masked(scores, 1.0 / math.sqrt(head_size),
+                                             mask.to(qkv.dtype).contiguous()).view(b * head_num, s, s)
     h = torch.bmm(attn, v)                                       # [b*h, s, d]
     return h.view(b, head_num, s, head_size).permute(0, 2, 1, 3).reshape(b, s, H).contiguous()
 
@@ -111,8 +132,7 @@ class BertLayer:
         H = self.heads * self.hsize
         if self._mask is None or self._mask.device != qkv_kernel.device:
             self._mask = causal_mask(s, qkv_kernel.device, qkv_kernel.dtype)
-        qkv = qkv_kernel + w.qkv_bias
-        h = attention_core(qkv, self.heads, self.hsize, self._mask).view(b * s, H)
+        h = attention_core(qkv_kernel, self.heads, self.hsize, self._mask, bias=w.qkv_bias).view(b * s, H)
         x1 = self.attn_out(h, w.attr_output_kernel, w.attr_output_bias, w.attr_output_layernorm_gamma,
                            w.attr_output_layernorm_beta, residual=input_tensor.reshape(b * s, H))
         inter = self.ffn_in(x1, w.inter_kernel, w.inter_bias)

@@ -167,11 +167,15 @@ layernorm_fwd_kernel(const T* X, const T* R, const T* __restrict__ W, const T* _
 
 // ---------------------------------------------------------------------------
 // Softmax over each row: exp(x - max) / sum (reference softmax_kernel; the
-// arithmetic is fp32 whatever the storage type).
+// arithmetic is fp32 whatever the storage type).  SCALED: the row is first
+// x * scale + mask[row % mask_rows] (mask [mask_rows, N], row stride N, or null):
+// the attention scores of the BERT layer (end2end.py:52-66: q k^T / sqrt(d) +
+// causal mask, then softmax) in one pass.
 // ---------------------------------------------------------------------------
-template <typename T, int VEC, int CPT>
+template <typename T, int VEC, int CPT, bool SCALED>
 __global__ void __launch_bounds__(1024)
-softmax_kernel(const T* __restrict__ X, T* __restrict__ Y, int M, int N, int ldx, int ldy, int tpr) {
+softmax_kernel(const T* __restrict__ X, T* __restrict__ Y, int M, int N, int ldx, int ldy, int tpr,
+               const T* __restrict__ mask, float scale, int mask_rows) {
   __shared__ float red[2][MAX_WAVES];
   int slot = 0;
   const int rpb = blockDim.x / tpr;
@@ -186,6 +190,12 @@ softmax_kernel(const T* __restrict__ X, T* __restrict__ Y, int M, int N, int ldx
     const int c = t + i * tpr;
     if (live && c < nch) {
       load_chunk<T, VEC>(X + (size_t)row * ldx + (size_t)c * VEC, x[i]);
+      if constexpr (SCALED) {
+        float mk[VEC];
+        if (mask != nullptr) load_chunk<T, VEC>(mask + (size_t)(row % mask_rows) * N + (size_t)c * VEC, mk);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[i][e] = x[i][e] * scale + (mask != nullptr ? mk[e] : 0.f);
+      }
 #pragma unroll
       for (int e = 0; e < VEC; ++e) m = fmaxf(m, x[i][e]);
     }
@@ -588,16 +598,23 @@ int ln_fwd_t(const void* X, const void* R, const void* W, const void* B, void* Y
 }
 
 template <typename T>
-int softmax_t(const void* X, void* Y, int M, int N, int ldx, int ldy, hipStream_t s) {
+int softmax_t(const void* X, void* Y, int M, int N, int ldx, int ldy, hipStream_t s, bool scaled = false,
+              const void* mask = nullptr, float scale = 1.f, int mask_rows = 1) {
   constexpr int V = 16 / (int)sizeof(T);
-  const bool vec_ok = N % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(X) && aligned16(Y);
+  const bool vec_ok = N % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(X) && aligned16(Y) &&
+                      (mask == nullptr || aligned16(mask));
   RowGeom g;
   if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 8 : 16, &g)) return set_error(ICPP_E_SHAPE, "icpp_softmax: N too large");
   const int rpb = g.block / g.tpr;
   const dim3 grid((M + rpb - 1) / rpb);
   hipError_t e = dispatch_cpt<T>(g, [&](auto VEC, auto CPT) {
-    hipLaunchKernelGGL((softmax_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), grid, dim3(g.block), 0, s,
-                       (const T*)X, (T*)Y, M, N, ldx, ldy, g.tpr);
+    constexpr int Vv = decltype(VEC)::value, Cc = decltype(CPT)::value;
+    if (scaled)
+      hipLaunchKernelGGL((softmax_kernel<T, Vv, Cc, true>), grid, dim3(g.block), 0, s, (const T*)X, (T*)Y, M, N, ldx,
+                         ldy, g.tpr, (const T*)mask, scale, mask_rows);
+    else
+      hipLaunchKernelGGL((softmax_kernel<T, Vv, Cc, false>), grid, dim3(g.block), 0, s, (const T*)X, (T*)Y, M, N, ldx,
+                         ldy, g.tpr, (const T*)nullptr, 1.f, 1);
     return hipGetLastError();
   });
   return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
@@ -715,6 +732,20 @@ int icpp_softmax(int dtype, const void* X, void* Y, int M, int N, int ldx, int l
   if (dtype == ICPP_F16) return softmax_t<_Float16>(X, Y, M, N, ldx, ldy, s);
   if (dtype == ICPP_BF16) return softmax_t<__bf16>(X, Y, M, N, ldx, ldy, s);
   return softmax_t<float>(X, Y, M, N, ldx, ldy, s);
+}
+
+int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* mask, float scale, int M, int N, int ldx,
+                               int ldy, int mask_rows, void* stream) {
+  if (!X || !Y) return set_error(ICPP_E_ARG, "icpp_softmax_scaled_masked: null tensor");
+  if (int rc = check_rows("icpp_softmax_scaled_masked: bad dtype or shape", dtype, M, N, ldx, ldy)) return rc;
+  if (mask != nullptr && mask_rows <= 0) return set_error(ICPP_E_SHAPE, "icpp_softmax_scaled_masked: mask_rows must be > 0");
+  if (!(scale == scale) || scale == INFINITY || scale == -INFINITY)
+    return set_error(ICPP_E_ARG, "icpp_softmax_scaled_masked: scale must be finite");
+  hipStream_t s = (hipStream_t)stream;
+  const int mr = mask != nullptr ? mask_rows : 1;
+  if (dtype == ICPP_F16) return softmax_t<_Float16>(X, Y, M, N, ldx, ldy, s, true, mask, scale, mr);
+  if (dtype == ICPP_BF16) return softmax_t<__bf16>(X, Y, M, N, ldx, ldy, s, true, mask, scale, mr);
+  return softmax_t<float>(X, Y, M, N, ldx, ldy, s, true, mask, scale, mr);
 }
 
 }  // extern "C"

@@ -216,5 +216,29 @@ def softmax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor
     return out
 
 
+def softmax_scaled_masked(x: torch.Tensor, scale: float, mask: Optional[torch.Tensor] = None,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(x * scale + mask) over the last dimension through icpp_softmax_scaled_masked.
+    x: [..., R, N] rows; mask: [R, N] in x's dtype (broadcast over the leading dims), or None."""
+    x2 = _rows(x, "x")
+    M, N = x2.shape
+    if out is None:
+        out = torch.empty_like(x)
+    y2 = _rows(out, "out")
+    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    pm, rows = None, 1
+    if mask is not None:
+        if mask.dtype != x.dtype or mask.dim() != 2 or mask.shape[1] != N or not mask.is_contiguous():
+            raise ValueError(f"mask must be a contiguous [R, {N}] {x.dtype} tensor")
+        if M % mask.shape[0]:
+            raise ValueError("the number of rows must be a multiple of the mask's")
+        pm, rows = mask.data_ptr(), mask.shape[0]
+    lib().call("icpp_softmax_scaled_masked", DTYPE[ROW_DTYPE[x.dtype]], x2.data_ptr(), y2.data_ptr(), pm,
+               float(scale), M, N, x2.stride(0), y2.stride(0), rows, _stream())
+    return out
+
+
 __all__ = ["BIAS_DTYPE", "OUT_DTYPE", "ROW_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
-           "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "softmax", "workspace_bytes"]
+           "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "softmax", "softmax_scaled_masked",
+           "workspace_bytes"]

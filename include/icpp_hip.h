@@ -196,6 +196,16 @@ int icpp_layernorm_bwd(int dtype, const void* DY, const void* X, const void* W,
  */
 int icpp_softmax(int dtype, const void* X, void* Y, int M, int N, int ldx, int ldy, void* stream);
 
+/*
+ * Y = softmax(X * scale + mask[row % mask_rows]) per row, in one pass: the
+ * attention scores of the reference's BERT layer (evaluation/end2end.py:52-66:
+ * matmul(q, k^T) / sqrt(head_size) + causal mask, then softmax).  mask is
+ * [mask_rows, N] in X's dtype with row stride N, or null (scale only); the
+ * arithmetic is fp32.  Same shape limits as icpp_softmax.
+ */
+int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* mask, float scale, int M, int N,
+                               int ldx, int ldy, int mask_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -130,6 +130,17 @@ def softmax_ref(x):
     return num / num.sum(dim=-1, keepdim=True)
 
 
+def softmax_scaled_masked_ref(x, scale: float, mask=None):
+    """softmax(x * scale + mask[row % R]) in fp32 over the last dimension: the attention
+    scores of evaluation/end2end.py (:52-66, matmul / sqrt(d) + mask, then softmax) for a
+    [rows, N] score matrix whose rows repeat the [R, N] mask (rows = batch*heads*R)."""
+    z = x.float().cpu() * scale
+    if mask is not None:
+        m = mask.float().cpu()
+        z = z + m.repeat(z.shape[0] // m.shape[0], 1)
+    return softmax_ref(z)
+
+
 def bert_layer_ref(qkv_kernel, input_tensor, w, head_num: int, head_size: int, eps: float = 1e-5):
     """One BERT encoder layer in fp32, as evaluation/end2end.py bert_fwd_std (:47-87):
     qkv = qkv_kernel + qkv_bias; per head scores = q k^T / sqrt(d) + causal mask

@@ -133,6 +133,11 @@ def test_rowops_validation_errors_before_launch(L):
     assert fwd(f16, 16, 16, 16, 16, None, None, 4, 1 << 17, 1 << 17, 1 << 17, eps, None) == -2  # row too long
     assert sm(f32, None, 16, 4, 64, 64, 64, None) == -4
     assert sm(f32, 16, 16, 4, 20000, 20001, 20001, None) == -2                        # scalar path limit 16384
+    smm = L._dll.icpp_softmax_scaled_masked
+    assert smm(f32, None, 16, None, 1.0, 4, 64, 64, 64, 1, None) == -4                  # null x
+    assert smm(f32, 16, 16, 16, 1.0, 4, 64, 64, 64, 0, None) == -2                      # mask without rows
+    assert smm(f32, 16, 16, None, float("inf"), 4, 64, 64, 64, 1, None) == -4          # non-finite scale
+    assert smm(f32, 16, 16, None, float("nan"), 4, 64, 64, 64, 1, None) == -4
     ws = L.layernorm_bwd_workspace_bytes
     # N = 8192 f16: one 16-byte chunk per thread, 1024 threads = one row per workgroup
     assert ws(f16, 4096, 8192, 8192) == 256 * 2 * 8192 * 4

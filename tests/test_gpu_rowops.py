@@ -148,3 +148,27 @@ def test_softmax_strided_rows(gpu):
     torch.cuda.synchronize()
     _close(ys, O.softmax_ref(x), 1e-8, 1e-5, "strided")
     assert torch.equal(ys, y)
+
+
+@pytest.mark.parametrize("rows,R,N,dt", [(12 * 128, 128, 128, "f16"), (8 * 64, 64, 64, "bf16"),
+                                         (6 * 20, 20, 1000, "f32"), (5 * 8, 8, 781, "f16")])
+def test_softmax_scaled_masked(gpu, rows, R, N, dt):
+    """softmax(x * scale + mask[row % R]) (the BERT layer's attention scores) against the oracle;
+    N = 781 takes the per-element path.  Tolerances as test_softmax."""
+    dtype = DT[dt]
+    g = torch.Generator().manual_seed(300 + N)
+    x = (4.0 * torch.randn(rows, N, generator=g)).to(dtype)
+    mask = torch.triu(torch.full((R, N), -10000.0), 1).to(dtype)
+    scale = 0.125
+    print(f"[parity] softmax_scaled_masked rows={rows} R={R} N={N} {dt}", flush=True)
+    y = runtime.softmax_scaled_masked(x.cuda(), scale, mask.cuda())
+    y0 = runtime.softmax_scaled_masked(x.cuda(), scale)
+    torch.cuda.synchronize()
+    want = O.softmax_scaled_masked_ref(x, scale, mask)
+    want0 = O.softmax_scaled_masked_ref(x, scale)
+    if dtype == torch.float32:
+        _close(y, want, 1e-8, 1e-5, f"masked softmax {rows}x{N}")
+        _close(y0, want0, 1e-8, 1e-5, f"scaled softmax {rows}x{N}")
+    else:
+        _close(y, want, 1e-6, ULP[dtype], f"masked softmax {rows}x{N} {dt}")
+        _close(y0, want0, 1e-6, ULP[dtype], f"scaled softmax {rows}x{N} {dt}")

@@ -304,6 +304,21 @@ def test_layernorm_special_cases():
     assert abs(float(dw.sum())) < 1e-5   # each row of xhat sums to 0, so with constant dy the columns of dw do too
 
 
+def test_softmax_scaled_masked_ref():
+    """Scale + repeated additive mask, then softmax: torch's softmax of the explicitly
+    broadcast scores (4 heads x 6 query rows), the plain softmax at scale 1 without a
+    mask, and a causal mask of -10000 zeroing the masked columns."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(24, 6, generator=g, dtype=torch.float64)
+    mask = torch.triu(torch.full((6, 6), -10000.0, dtype=torch.float64), 1)
+    want = torch.softmax(x.view(4, 6, 6) * 0.125 + mask, dim=-1).view(24, 6)
+    got = O.softmax_scaled_masked_ref(x, 0.125, mask)
+    torch.testing.assert_close(got.double(), want, rtol=1e-6, atol=1e-8)
+    assert torch.equal(O.softmax_scaled_masked_ref(x, 1.0), O.softmax_ref(x))
+    assert float(got.view(4, 6, 6)[:, 0, 1:].abs().max()) == 0.0   # row 0 sees only column 0
+    assert torch.allclose(got.view(4, 6, 6)[:, 0, 0], torch.ones(4))
+
+
 def test_softmax_ref_matches_torch_and_invariants():
     g = torch.Generator().manual_seed(33)
     x = torch.randn(19, 781, generator=g)                    # the reference test's row length
