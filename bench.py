@@ -103,8 +103,12 @@ def _load_traffic(workload: str):
         return None
 
 
-def bench_ops(quick: bool, only: str = ""):
-    """Every benchmark configuration: tuned config, TFLOP/s, fraction of its roofline."""
+def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
+    """Every benchmark configuration: tuned config, TFLOP/s, fraction of its roofline.
+
+    ``fixed_configs``: the JSON an earlier ``--op`` run printed; its rows' configs
+    are reused instead of tuning (profiler runs time what the plain run chose --
+    under a kernel tracer the tuner's own short timings are distorted)."""
     import torch
 
     from icpp_tuning_amd.autotuner.interface import benchmark_ms, tune
@@ -117,37 +121,52 @@ def bench_ops(quick: bool, only: str = ""):
 
     rows = []
     top_k = 2 if quick else 4
+    fixed = {}
+    if fixed_configs:
+        for r in json.loads(Path(fixed_configs).read_text().strip().splitlines()[-1])["ops"]:
+            if "raw_config" in r:
+                fixed[(r["op"], json.dumps(r["shape"], sort_keys=True))] = r["raw_config"]
 
     def record(op, desc, shape, flops, min_bytes, dtype, **extra):
         if only and not op.startswith(only):
             return
-        res = tune(desc, top_k=top_k, warmup=2, reps=10, budget_ms=60.0, **shape)
         # Timed over input copies whose total exceeds the 256 MiB MALL + L2, so
-        # every launch reads its operands from HBM.
+        # every launch reads its operands from HBM.  HBM-bound shapes are also tuned
+        # that way: with one resident input set the tuner would rank configs by
+        # cache-hot speed.
         copies = max(1, min(16, -(-(600 << 20) // max(1, min_bytes))))
+        peak = PEAK_FP8 if dtype == "fp8" else PEAK_BF16
+        hbm_bound = flops / min_bytes < peak * 1e3 / HBM_GBPS
+        given = fixed.get((op, json.dumps(shape, sort_keys=True)))
+        res = None if given is not None else tune(desc, top_k=top_k, warmup=2, reps=10, budget_ms=60.0,
+                                                  input_copies=copies if hbm_bound else 1, **shape)
+        best = given if given is not None else res.best_config
         sets = [desc.make_inputs(**shape) for _ in range(copies)]
-        runs = [desc.make_runner(res.best_config, inp, **shape) for inp in sets]
+        runs = [desc.make_runner(best, inp, **shape) for inp in sets]
         ms = benchmark_ms(runs, warmup=copies, reps=max(20, 2 * copies))
         del sets, runs
         tflops = flops / ms / 1e9
         gbps = min_bytes / ms / 1e6
-        peak = PEAK_FP8 if dtype == "fp8" else PEAK_BF16
-        ridge = peak * 1e3 / HBM_GBPS
-        bound = "mfma" if flops / min_bytes >= ridge else "hbm"
-        row = {"op": op, "shape": shape, "dtype": dtype, "config": desc.format_config(res.best_config),
-               "input_copies": copies,
-               "ms": round(ms, 5), "tflops": round(tflops, 2), "pct_mfma_peak": round(100 * tflops / peak, 2),
-               "gbps": round(gbps, 1), "pct_hbm": round(100 * gbps / HBM_GBPS, 2), "bound": bound,
-               "formula_top1": desc.format_config(res.formula_top1),
-               "formula_top1_ms": round(res.formula_top1_ms, 5),
-               "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),
-                         "compile_s": round(res.compile_s, 4), "bench_s": round(res.bench_s, 3),
-                         "candidates": len(res.candidates), "n_configs": res.n_configs, "n_pruned": res.n_pruned}}
+        bound = "hbm" if hbm_bound else "mfma"
+        row = {"op": op, "shape": shape, "dtype": dtype, "config": desc.format_config(best), "raw_config": best,
+               "input_copies": copies, "ms": round(ms, 5), "tflops": round(tflops, 2),
+               "pct_mfma_peak": round(100 * tflops / peak, 2),
+               "gbps": round(gbps, 1), "pct_hbm": round(100 * gbps / HBM_GBPS, 2), "bound": bound}
+        if res is None:
+            row["config_from"] = fixed_configs
+        else:
+            row.update({
+                "tuned_over_copies": copies if hbm_bound else 1,
+                "formula_top1": desc.format_config(res.formula_top1),
+                "formula_top1_ms": round(res.formula_top1_ms, 5),
+                "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),
+                          "compile_s": round(res.compile_s, 4), "bench_s": round(res.bench_s, 3),
+                          "candidates": len(res.candidates), "n_configs": res.n_configs, "n_pruned": res.n_pruned}})
         row.update(extra)
         rows.append(row)
+        how = f"tuned in {res.time_to_best_s:.2f}s" if res is not None else "config given"
         print(f"[bench] {op} {shape} {row['config']}: {ms*1e3:.1f} us, {tflops:.1f} TFLOP/s "
-              f"({row['pct_mfma_peak']}% peak), {gbps:.0f} GB/s, tuned in {res.time_to_best_s:.2f}s",
-              file=sys.stderr, flush=True)
+              f"({row['pct_mfma_peak']}% peak), {gbps:.0f} GB/s, {how}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 
     M = N = K = 1024
@@ -284,6 +303,8 @@ def main():
                     help="time this compiled GEMM instance (by name) instead of the tuned one")
     ap.add_argument("--op", default="",
                     help="per-op table only, for the ops whose name starts with this (e.g. conv2d, gemm_bias_layernorm)")
+    ap.add_argument("--op-configs", default="",
+                    help="with --op: reuse the configs of an earlier --op run's JSON instead of tuning")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
     args = ap.parse_args()
@@ -313,7 +334,7 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     if args.op:  # one family of per-op rows only (profiling runs)
-        print(json.dumps({"ops": bench_ops(args.quick, args.op)}), flush=True)
+        print(json.dumps({"ops": bench_ops(args.quick, args.op, args.op_configs)}), flush=True)
         return 0
     M = N = K = 4096
     desc = GBA.descriptor("gelu_tanh", "bf16")
