@@ -131,15 +131,15 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
         if only and not op.startswith(only):
             return
         # Timed over input copies whose total exceeds the 256 MiB MALL + L2, so
-        # every launch reads its operands from HBM.  HBM-bound shapes are also tuned
-        # that way: with one resident input set the tuner would rank configs by
-        # cache-hot speed.
+        # every launch reads its operands from HBM, and tuned the same way: with one
+        # resident input set the tuner ranks configs by cache-hot speed (a conv tile
+        # that won warm at 14x14x256 ran 1.5x slower cold).
         copies = max(1, min(16, -(-(600 << 20) // max(1, min_bytes))))
         peak = PEAK_FP8 if dtype == "fp8" else PEAK_BF16
         hbm_bound = flops / min_bytes < peak * 1e3 / HBM_GBPS
         given = fixed.get((op, json.dumps(shape, sort_keys=True)))
         res = None if given is not None else tune(desc, top_k=top_k, warmup=2, reps=10, budget_ms=60.0,
-                                                  input_copies=copies if hbm_bound else 1, **shape)
+                                                  input_copies=copies, **shape)
         best = given if given is not None else res.best_config
         sets = [desc.make_inputs(**shape) for _ in range(copies)]
         runs = [desc.make_runner(best, inp, **shape) for inp in sets]
@@ -156,7 +156,7 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
             row["config_from"] = fixed_configs
         else:
             row.update({
-                "tuned_over_copies": copies if hbm_bound else 1,
+                "tuned_over_copies": copies,
                 "formula_top1": desc.format_config(res.formula_top1),
                 "formula_top1_ms": round(res.formula_top1_ms, 5),
                 "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),

@@ -80,7 +80,9 @@ def test_config4_fused(gpu, variant, shape):
 
 
 @pytest.mark.parametrize("geom", [
-    # (N, H, W, C, F, KH, KW, stride, pad, dilation): general gather, stride 2, 1x1 with a partial N tile
+    # (N, H, W, C, F, KH, KW, stride, pad, dilation): 3x3 with C = 2 x 64, general gather,
+    # stride 2, 1x1 with a partial N tile
+    (2, 9, 7, 128, 64, 3, 3, 1, 1, 1),
     (2, 7, 6, 16, 64, 2, 2, 1, 0, 1),
     (2, 9, 9, 64, 64, 3, 3, 2, 1, 1),
     (1, 5, 5, 128, 72, 1, 1, 1, 0, 1),

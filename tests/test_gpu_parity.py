@@ -255,7 +255,8 @@ def test_uneven_split_k(gpu, dtype, M, N, K, sk):
     assert ran > 0
 
 
-@pytest.mark.parametrize("shape,sk", [((32, 56, 56, 64, 64), 1), ((32, 14, 14, 256, 256), 2)])
+@pytest.mark.parametrize("shape,sk", [((32, 56, 56, 64, 64), 1), ((32, 14, 14, 256, 256), 2),
+                                      ((32, 14, 14, 256, 256), 1), ((32, 7, 7, 512, 512), 1)])
 def test_conv_every_instance_full_size(gpu, shape, sk):
     """Every conv tile at two benchmark sizes (many workgroup rounds for the small
     tiles), alone and with split-K."""
@@ -277,6 +278,8 @@ def test_conv_every_instance_full_size(gpu, shape, sk):
 
 @pytest.mark.parametrize("geom", [
     # (N, H, W, C, F, KH, KW, stride, pad, dilation)
+    (2, 9, 7, 128, 64, 3, 3, 1, 1, 1),   # 3x3 stride 1, C = 2 x 64: per-tile-tap gather, two tiles per tap
+    (3, 5, 5, 192, 72, 3, 3, 1, 1, 1),   # C = 3 x 64, F not a multiple of the tile
     (2, 7, 6, 16, 64, 2, 2, 1, 0, 1),    # K tile spans 4 filter taps (general gather path)
     (2, 9, 9, 64, 64, 3, 3, 2, 1, 1),    # stride 2
     (2, 8, 8, 64, 128, 3, 3, 1, 2, 2),   # dilation 2
