@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Any, Callable, Dict, List, Optional, Tuple
+from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
 from .cost_model import OpSpec, TuneConfig, score_formula, score_formula_detailed
 from .gpu_spec import GPUSpec, get_gpu_spec
@@ -202,8 +202,14 @@ def benchmark_ms(fn, warmup: int = 3, reps: int = 10, batches: int = 3, graph: b
     return times[len(times) // 2]
 
 
+def input_bytes(inputs: Any) -> int:
+    """Bytes of the device tensors in one input set (a dict / sequence of tensors)."""
+    vals = inputs.values() if isinstance(inputs, dict) else inputs
+    return sum(int(v.numel()) * int(v.element_size()) for v in vals if hasattr(v, "element_size"))
+
+
 def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: int = 4, warmup: int = 2,
-         reps: int = 5, budget_ms: float = 0.0, prune: bool = True, input_copies: int = 1,
+         reps: int = 5, budget_ms: float = 0.0, prune: bool = True, input_copies: Union[int, str] = 1,
          **shape_kwargs: Any) -> TuneResult:
     """Formula-rank, then measure candidates on the device and keep the fastest.
 
@@ -214,7 +220,8 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     set for the shape, as offline profiling does.  ``input_copies`` > 1 times
     every candidate round-robin over that many input sets, so an operand set
     that would otherwise stay resident in the 256 MiB MALL is read from HBM on
-    every launch -- the condition a memory-bound op is judged in.
+    every launch -- the condition a memory-bound op is judged in; "auto" picks
+    enough sets (at most 16) to exceed 600 MiB.
 
     time_to_best = prune+rank (host) + compile (instance lookup: kernels are AOT)
     + device benchmarks.  Generating the synthetic inputs is reported
@@ -228,8 +235,12 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     if not ranked:
         raise RuntimeError(f"No configs survive pruning for {descriptor.name} with {shape_kwargs}")
     t1 = time.perf_counter()
-    copies = max(1, int(input_copies))
-    inputs = [descriptor.make_inputs(**shape_kwargs) for _ in range(copies)]  # harness, not tuner work
+    inputs = [descriptor.make_inputs(**shape_kwargs)]  # benchmark harness, not tuner work
+    if input_copies == "auto":
+        copies = max(1, min(16, -(-(600 << 20) // max(1, input_bytes(inputs[0])))))
+    else:
+        copies = max(1, int(input_copies))
+    inputs += [descriptor.make_inputs(**shape_kwargs) for _ in range(copies - 1)]
     t_in = time.perf_counter()
     if copies > 1:
         warmup, reps = max(warmup, copies), max(reps, 2 * copies)
