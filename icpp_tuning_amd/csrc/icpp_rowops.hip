@@ -61,7 +61,7 @@ __device__ __forceinline__ void store_chunk(T* p, const float* in) {
     for (int i = 0; i < VEC; ++i) e[i] = from_f<T>(in[i]);
     i32x4 raw;
     __builtin_memcpy(&raw, e, 16);
-    *reinterpret_cast<i32x4*>(p) = raw;
+    __builtin_nontemporal_store(raw, reinterpret_cast<i32x4*>(p));
   }
 }
 
