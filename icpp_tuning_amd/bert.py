@@ -76,9 +76,11 @@ def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch
     """softmax(q k^T / sqrt(d) + mask) v over heads, [b, s, 3H] -> [b, s, H] (end2end.py:47-71),
     with q, k, v taken from qkv (+ bias, [3H], when given).
 
-    Default path: one strided add writes (qkv + bias) head-major as [3, b, h, s, d], the
-    scores come from one batched product, and icpp_softmax_scaled_masked applies the scale,
-    the additive mask and the softmax in one pass.  With ``softmax`` given (a row softmax),
+    Default path: icpp_qkv_split_heads writes q, k^T and v per head with the bias added
+    (head_size 64; other sizes use one strided add into [3, b, h, s, d] and a k copy), the
+    scores come from one batched product, icpp_softmax_scaled_masked applies the scale,
+    the additive mask and the softmax in one pass, and icpp_merge_heads lays the context
+    back out as [b, s, H].  With ``softmax`` given (a row softmax),
     the reference's order is kept op for op -- scale, mask add, softmax -- as the torch
     composition this layer is measured against."""
     b, s, _ = qkv.shape
@@ -94,18 +96,26 @@ def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch
         scores = (scores.view(b, head_num, s, s) + mask).reshape(b * head_num * s, s)
         attn = softmax(scores.contiguous()).view(b * head_num, s, s)
     else:
-        heads = qkv.view(b, s, 3, head_num, head_size).permute(2, 0, 3, 1, 4)   # [3, b, h, s, d] view
-        t = torch.empty((3, b, head_num, s, head_size), dtype=qkv.dtype, device=qkv.device)
-        if bias is not None:
-            torch.add(heads, bias.view(3, 1, head_num, 1, head_size), out=t)
+        fused = head_size == runtime.HEAD_DIM and qkv.dtype in (torch.float16, torch.bfloat16)
+        if fused:
+            q, k, v = runtime.qkv_split_heads(qkv.contiguous(), head_num, bias)   # k: [b*h, d, s]
         else:
-            t.copy_(heads)
-        q = t[0].view(b * head_num, s, head_size)
-        v = t[2].view(b * head_num, s, head_size)
-        k = t[1].view(b * head_num, s, head_size).transpose(1, 2).contiguous()    # [b*h, d, s]
+            heads = qkv.view(b, s, 3, head_num, head_size).permute(2, 0, 3, 1, 4)   # [3, b, h, s, d] view
+            t = torch.empty((3, b, head_num, s, head_size), dtype=qkv.dtype, device=qkv.device)
+            if bias is not None:
+                torch.add(heads, bias.view(3, 1, head_num, 1, head_size), out=t)
+            else:
+                t.copy_(heads)
+            q = t[0].view(b * head_num, s, head_size)
+            v = t[2].view(b * head_num, s, head_size)
+            k = t[1].view(b * head_num, s, head_size).transpose(1, 2).contiguous()    # [b*h, d, s]
         scores = torch.bmm(q, k).view(b * head_num * s, s)
         attn = runtime.softmax_scaled_masked(scores, 1.0 / math.sqrt(head_size),
                                              mask.to(qkv.dtype).contiguous()).view(b * head_num, s, s)
+        h = torch.bmm(attn, v)                                   # [b*h, s, d]
+        if fused:
+            return runtime.merge_heads(h, b)
+        return h.view(b, head_num, s, head_size).permute(0, 2, 1, 3).reshape(b, s, H).contiguous()
     h = torch.bmm(attn, v)                                       # [b*h, s, d]
     return h.view(b, head_num, s, head_size).permute(0, 2, 1, 3).reshape(b, s, H).contiguous()
 

@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "icpp_hip.h"
 
 namespace icpp_rows {
@@ -516,6 +518,91 @@ layernorm_dwdb_kernel(const float* __restrict__ part, T* __restrict__ DW, T* __r
   }
 }
 
+// ---------------------------------------------------------------------------
+// Attention head layout (BERT attention core, head_dim 64)
+// ---------------------------------------------------------------------------
+// qkv_split_heads: the fused QKV projection [T = batch*seq, 3*H] (H = heads*64) plus
+// its bias [3H] -> Q [batch, heads, seq, 64], K^T [batch, heads, 64, seq] and
+// V [batch, heads, seq, 64].  A workgroup takes 64 rows of one (batch, head): it
+// reads three 64 x 64 blocks (one 128-byte row segment per token), adds the bias
+// in fp32 and rounds once (as torch's add of two 16-bit tensors), writes Q and V
+// as contiguous 8 KiB blocks and K through a padded LDS tile (row stride 66
+// elements, so a column read spreads over the banks) as 64 rows of 64 tokens.
+// Every access is a 16-byte chunk; rows past seq are neither read nor written.
+constexpr int HD = 64;            // head_dim this kernel serves
+constexpr int KT_LD = HD + 2;     // LDS tile row stride (elements)
+template <typename T>
+__global__ void __launch_bounds__(256)
+qkv_split_heads_kernel(const T* __restrict__ QKV, const T* __restrict__ bias, T* __restrict__ Q,
+                       T* __restrict__ KT, T* __restrict__ V, int seq, int heads) {
+  __shared__ T kt[HD][KT_LD];
+  const int s0 = blockIdx.x * HD, hh = blockIdx.y, bb = blockIdx.z;
+  const int H = heads * HD;
+  const size_t bh = (size_t)bb * heads + hh;
+  // chunk q = tid + 256 * i of the 64 x 8 block: token row q / 8, 8-element chunk q % 8
+#pragma unroll
+  for (int part = 0; part < 3; ++part) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int r = q >> 3, c = q & 7;
+      const int ss = s0 + r;
+      if (ss >= seq) continue;
+      const int col = part * H + hh * HD + c * 8;
+      float v[8];
+      load_chunk<T, 8>(QKV + ((size_t)bb * seq + ss) * (3 * (size_t)H) + col, v);
+      if (bias != nullptr) {
+        float bv[8];
+        load_chunk<T, 8>(bias + col, bv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += bv[e];
+      }
+      if (part == 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kt[c * 8 + e][r] = from_f<T>(v[e]);
+      } else {
+        store_chunk<T, 8>((part == 0 ? Q : V) + (bh * seq + ss) * HD + c * 8, v);
+      }
+    }
+  }
+  __syncthreads();
+  // K^T rows: head dim d, 64 tokens s0 .. s0+63 (8 chunks of 8 tokens)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    const int d = q >> 3, c = q & 7;
+    const int ss = s0 + c * 8;
+    if (ss >= seq) continue;
+    T* out = KT + (bh * HD + d) * (size_t)seq + ss;
+    if (ss + 8 <= seq && (seq & 7) == 0) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = to_f(kt[d][c * 8 + e]);
+      store_chunk<T, 8>(out, v);
+    } else {
+      for (int e = 0; e < 8 && ss + e < seq; ++e) out[e] = kt[d][c * 8 + e];
+    }
+  }
+}
+
+// merge_heads: context [batch, heads, seq, 64] -> [batch*seq, heads*64], one 16-byte
+// chunk per lane, consecutive lanes on consecutive chunks of an output row.
+template <typename T>
+__global__ void __launch_bounds__(256)
+merge_heads_kernel(const T* __restrict__ X, T* __restrict__ Y, int batch, int seq, int heads) {
+  const size_t chunks = (size_t)batch * seq * heads * (HD / 8);
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < chunks; q += stride) {
+    const int c = (int)(q % (HD / 8));
+    const size_t rest = q / (HD / 8);
+    const int hh = (int)(rest % heads);
+    const size_t t = rest / heads;  // token row bb * seq + ss
+    const size_t bb = t / seq, ss = t % seq;
+    const i32x4 v = *reinterpret_cast<const i32x4*>(X + ((bb * heads + hh) * seq + ss) * HD + c * 8);
+    __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(Y + t * ((size_t)heads * HD) + hh * HD + c * 8));
+  }
+}
+
 }  // namespace icpp_rows
 
 // ---------------------------------------------------------------------------
@@ -746,6 +833,49 @@ int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* ma
   if (dtype == ICPP_F16) return softmax_t<_Float16>(X, Y, M, N, ldx, ldy, s, true, mask, scale, mr);
   if (dtype == ICPP_BF16) return softmax_t<__bf16>(X, Y, M, N, ldx, ldy, s, true, mask, scale, mr);
   return softmax_t<float>(X, Y, M, N, ldx, ldy, s, true, mask, scale, mr);
+}
+
+// Attention head layout (head_dim 64): see qkv_split_heads_kernel / merge_heads_kernel.
+int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* KT, void* V, int batch,
+                         int seq, int heads, int head_dim, void* stream) {
+  if (!QKV || !Q || !KT || !V) return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: null tensor");
+  if (dtype != ICPP_F16 && dtype != ICPP_BF16) return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: dtype must be f16 or bf16");
+  if (head_dim != HD) return set_error(ICPP_E_SHAPE, "icpp_qkv_split_heads: head_dim must be 64");
+  if (batch <= 0 || seq <= 0 || heads <= 0 || (long long)batch * seq * heads * 3 * HD > 0x7FFFFFFFll)
+    return set_error(ICPP_E_SHAPE, "icpp_qkv_split_heads: bad or too large shape");
+  if (!aligned16(QKV) || (bias && !aligned16(bias)) || !aligned16(Q) || !aligned16(KT) || !aligned16(V))
+    return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: pointers must be 16-byte aligned");
+  const dim3 grid((seq + HD - 1) / HD, heads, batch);
+  if (batch > 65535 || heads > 65535) return set_error(ICPP_E_SHAPE, "icpp_qkv_split_heads: grid too large");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ICPP_F16)
+    hipLaunchKernelGGL(qkv_split_heads_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16*)QKV,
+                       (const _Float16*)bias, (_Float16*)Q, (_Float16*)KT, (_Float16*)V, seq, heads);
+  else
+    hipLaunchKernelGGL(qkv_split_heads_kernel<__bf16>, grid, dim3(256), 0, s, (const __bf16*)QKV,
+                       (const __bf16*)bias, (__bf16*)Q, (__bf16*)KT, (__bf16*)V, seq, heads);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
+}
+
+int icpp_merge_heads(int dtype, const void* X, void* Y, int batch, int seq, int heads, int head_dim, void* stream) {
+  if (!X || !Y) return set_error(ICPP_E_ARG, "icpp_merge_heads: null tensor");
+  if (dtype != ICPP_F16 && dtype != ICPP_BF16) return set_error(ICPP_E_ARG, "icpp_merge_heads: dtype must be f16 or bf16");
+  if (head_dim != HD) return set_error(ICPP_E_SHAPE, "icpp_merge_heads: head_dim must be 64");
+  if (batch <= 0 || seq <= 0 || heads <= 0 || (long long)batch * seq * heads * HD > 0x7FFFFFFFll)
+    return set_error(ICPP_E_SHAPE, "icpp_merge_heads: bad or too large shape");
+  if (!aligned16(X) || !aligned16(Y)) return set_error(ICPP_E_ARG, "icpp_merge_heads: pointers must be 16-byte aligned");
+  const long long chunks = (long long)batch * seq * heads * (HD / 8);
+  const int blocks = (int)std::min<long long>((chunks + 255) / 256, 4096);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ICPP_F16)
+    hipLaunchKernelGGL(merge_heads_kernel<_Float16>, dim3(blocks), dim3(256), 0, s, (const _Float16*)X, (_Float16*)Y,
+                       batch, seq, heads);
+  else
+    hipLaunchKernelGGL(merge_heads_kernel<__bf16>, dim3(blocks), dim3(256), 0, s, (const __bf16*)X, (__bf16*)Y,
+                       batch, seq, heads);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
 }
 
 }  // extern "C"

@@ -239,6 +239,41 @@ def softmax_scaled_masked(x: torch.Tensor, scale: float, mask: Optional[torch.Te
     return out
 
 
-__all__ = ["BIAS_DTYPE", "OUT_DTYPE", "ROW_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
-           "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "softmax", "softmax_scaled_masked",
-           "workspace_bytes"]
+HEAD_DIM = 64  # head size the attention layout kernels serve
+
+
+def qkv_split_heads(qkv: torch.Tensor, heads: int, bias: Optional[torch.Tensor] = None):
+    """[batch, seq, 3*heads*64] (+ bias [3*heads*64]) -> (q [batch*heads, seq, 64],
+    k^T [batch*heads, 64, seq], v [batch*heads, seq, 64]) through icpp_qkv_split_heads
+    (end2end.py:48-58: qkv + bias, chunk, transpose_for_scores, permute, k rearranged)."""
+    if qkv.dim() != 3 or qkv.dtype not in (torch.float16, torch.bfloat16) or not qkv.is_contiguous():
+        raise ValueError("qkv_split_heads: qkv must be a contiguous [batch, seq, 3H] f16 / bf16 tensor")
+    b, s, w = qkv.shape
+    if w != 3 * heads * HEAD_DIM:
+        raise ValueError(f"qkv_split_heads: last dim {w} != 3 * heads * {HEAD_DIM}")
+    if bias is not None and (bias.dtype != qkv.dtype or not bias.is_contiguous() or bias.numel() != w):
+        raise ValueError("qkv_split_heads: bias must be a contiguous [3H] tensor of qkv's dtype")
+    q = torch.empty((b * heads, s, HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
+    kt = torch.empty((b * heads, HEAD_DIM, s), dtype=qkv.dtype, device=qkv.device)
+    v = torch.empty_like(q)
+    lib().call("icpp_qkv_split_heads", DTYPE[ROW_DTYPE[qkv.dtype]], qkv.data_ptr(),
+               bias.data_ptr() if bias is not None else None, q.data_ptr(), kt.data_ptr(), v.data_ptr(),
+               b, s, heads, HEAD_DIM, _stream())
+    return q, kt, v
+
+
+def merge_heads(ctx: torch.Tensor, batch: int) -> torch.Tensor:
+    """[batch*heads, seq, 64] -> [batch, seq, heads*64] through icpp_merge_heads (end2end.py:68-71)."""
+    if ctx.dim() != 3 or ctx.shape[2] != HEAD_DIM or ctx.dtype not in (torch.float16, torch.bfloat16) \
+            or not ctx.is_contiguous() or ctx.shape[0] % batch:
+        raise ValueError("merge_heads: ctx must be a contiguous [batch*heads, seq, 64] f16 / bf16 tensor")
+    heads, s = ctx.shape[0] // batch, ctx.shape[1]
+    y = torch.empty((batch, s, heads * HEAD_DIM), dtype=ctx.dtype, device=ctx.device)
+    lib().call("icpp_merge_heads", DTYPE[ROW_DTYPE[ctx.dtype]], ctx.data_ptr(), y.data_ptr(), batch, s, heads,
+               HEAD_DIM, _stream())
+    return y
+
+
+__all__ = ["BIAS_DTYPE", "HEAD_DIM", "OUT_DTYPE", "ROW_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
+           "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "merge_heads", "qkv_split_heads", "softmax",
+           "softmax_scaled_masked", "workspace_bytes"]

@@ -206,6 +206,21 @@ int icpp_softmax(int dtype, const void* X, void* Y, int M, int N, int ldx, int l
 int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* mask, float scale, int M, int N,
                                int ldx, int ldy, int mask_rows, void* stream);
 
+/*
+ * Attention head layout of the reference's BERT layer, head_dim 64 (f16 / bf16).
+ * icpp_qkv_split_heads replaces `qkv + qkv_bias`, `chunk(3)`, transpose_for_scores
+ * and the three permute(0, 2, 1, 3).contiguous() copies plus the k rearrange to
+ * [(b h), d, s] (evaluation/end2end.py:48-58): QKV [batch*seq, 3*heads*64] row-major
+ * (+ bias [3*heads*64], or null) -> Q and V [batch, heads, seq, 64], KT
+ * [batch, heads, 64, seq]; the bias add is one fp32 add rounded to the dtype.
+ * icpp_merge_heads replaces the context reshape back to [batch*seq, heads*64]
+ * (end2end.py:68-71): X [batch, heads, seq, 64] -> Y [batch*seq, heads*64].
+ * Pointers 16-byte aligned; batch*seq*heads*3*64 below 2^31.
+ */
+int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* KT, void* V, int batch,
+                         int seq, int heads, int head_dim, void* stream);
+int icpp_merge_heads(int dtype, const void* X, void* Y, int batch, int seq, int heads, int head_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

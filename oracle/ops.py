@@ -141,6 +141,29 @@ def softmax_scaled_masked_ref(x, scale: float, mask=None):
     return softmax_ref(z)
 
 
+def qkv_split_heads_ref(qkv, heads: int, bias=None):
+    """evaluation/end2end.py:48-58 on the CPU: qkv + bias (rounded to qkv's dtype), chunk(3),
+    transpose_for_scores, permute(0, 2, 1, 3) and k rearranged to '(b h) d s'.
+    qkv [b, s, 3H] -> (q [b*h, s, d], k^T [b*h, d, s], v [b*h, s, d]), d = H / heads."""
+    x = qkv.cpu()
+    if bias is not None:
+        x = (x.float() + bias.cpu().float()).to(qkv.dtype)
+    b, s, w = x.shape
+    d = w // 3 // heads
+    q1, k1, v1 = x.chunk(3, dim=-1)
+    per_head = [t.reshape(b, s, heads, d).permute(0, 2, 1, 3).reshape(b * heads, s, d).contiguous()
+                for t in (q1, k1, v1)]
+    return per_head[0], per_head[1].transpose(1, 2).contiguous(), per_head[2]
+
+
+def merge_heads_ref(ctx, batch: int):
+    """[batch*heads, s, d] -> [batch, s, heads*d] (end2end.py:68-71: the context's
+    'b h t d -> b t (h d)' reshape), on the CPU."""
+    x = ctx.cpu()
+    bh, s, d = x.shape
+    return x.reshape(batch, bh // batch, s, d).permute(0, 2, 1, 3).reshape(batch, s, bh // batch * d).contiguous()
+
+
 def bert_layer_ref(qkv_kernel, input_tensor, w, head_num: int, head_size: int, eps: float = 1e-5):
     """One BERT encoder layer in fp32, as evaluation/end2end.py bert_fwd_std (:47-87):
     qkv = qkv_kernel + qkv_bias; per head scores = q k^T / sqrt(d) + causal mask

@@ -138,6 +138,15 @@ def test_rowops_validation_errors_before_launch(L):
     assert smm(f32, 16, 16, 16, 1.0, 4, 64, 64, 64, 0, None) == -2                      # mask without rows
     assert smm(f32, 16, 16, None, float("inf"), 4, 64, 64, 64, 1, None) == -4          # non-finite scale
     assert smm(f32, 16, 16, None, float("nan"), 4, 64, 64, 64, 1, None) == -4
+    qs, mh = L._dll.icpp_qkv_split_heads, L._dll.icpp_merge_heads
+    assert qs(f16, None, None, 16, 16, 16, 2, 128, 12, 64, None) == -4                 # null qkv
+    assert qs(f16, 16, None, 16, 16, 16, 2, 128, 12, 32, None) == -2                   # head_dim 64 only
+    assert qs(f32, 16, None, 16, 16, 16, 2, 128, 12, 64, None) == -4                   # f16 / bf16 only
+    assert qs(f16, 24, None, 16, 16, 16, 2, 128, 12, 64, None) == -4                   # misaligned
+    assert qs(f16, 16, None, 16, 16, 16, 0, 128, 12, 64, None) == -2                   # empty
+    assert mh(f16, 16, 16, 2, 128, 12, 48, None) == -2
+    assert mh(f16, 16, None, 2, 128, 12, 64, None) == -4
+    assert "icpp_merge_heads" in L.last_error()
     ws = L.layernorm_bwd_workspace_bytes
     # N = 8192 f16: one 16-byte chunk per thread, 1024 threads = one row per workgroup
     assert ws(f16, 4096, 8192, 8192) == 256 * 2 * 8192 * 4

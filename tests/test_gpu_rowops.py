@@ -172,3 +172,26 @@ def test_softmax_scaled_masked(gpu, rows, R, N, dt):
     else:
         _close(y, want, 1e-6, ULP[dtype], f"masked softmax {rows}x{N} {dt}")
         _close(y0, want0, 1e-6, ULP[dtype], f"scaled softmax {rows}x{N} {dt}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b,s,heads,with_bias", [(2, 128, 12, True), (3, 100, 4, True), (1, 37, 2, False),
+                                                  (4, 64, 1, True), (1, 1, 3, True)])
+def test_qkv_split_and_merge_heads(gpu, dtype, b, s, heads, with_bias):
+    """icpp_qkv_split_heads / icpp_merge_heads against the CPU restatement, bit for bit:
+    sequence tiles of 64 with a partial last one (100), lengths off the 8-token chunk
+    (37, 1: the element-wise K^T path), no bias, one head."""
+    g = torch.Generator().manual_seed(b * 1000 + s * 10 + heads)
+    H = heads * 64
+    qkv = (torch.rand(b, s, 3 * H, generator=g) * 4 - 2).to(dtype)
+    bias = (torch.rand(3 * H, generator=g) - 0.5).to(dtype) if with_bias else None
+    want = O.qkv_split_heads_ref(qkv, heads, bias)
+    print(f"[parity] qkv_split_heads b={b} s={s} heads={heads} {dtype} bias={with_bias}", flush=True)
+    got = runtime.qkv_split_heads(qkv.cuda(), heads, bias.cuda() if bias is not None else None)
+    torch.cuda.synchronize()
+    for name, w, o in zip(("q", "k^T", "v"), want, got):
+        assert torch.equal(o.cpu().view(torch.int16), w.view(torch.int16)), name
+    ctx = (torch.rand(b * heads, s, 64, generator=g) - 0.5).to(dtype)
+    y = runtime.merge_heads(ctx.cuda(), b)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu().view(torch.int16), O.merge_heads_ref(ctx, b).view(torch.int16))

@@ -319,6 +319,28 @@ def test_softmax_scaled_masked_ref():
     assert torch.allclose(got.view(4, 6, 6)[:, 0, 0], torch.ones(4))
 
 
+def test_qkv_split_and_merge_heads_ref():
+    """Head layout by explicit indexing on a tiny case (2 batches, 3 tokens, 2 heads of 4):
+    q[b*h + i, t, e] = qkv[b, t, i*d + e] + bias, k^T[b*h + i, e, t] and v from the second
+    and third thirds; merging q back gives the first third of qkv + bias."""
+    g = torch.Generator().manual_seed(5)
+    B, S, Hn, D = 2, 3, 2, 4
+    qkv = torch.randn(B, S, 3 * Hn * D, generator=g).half()
+    bias = torch.randn(3 * Hn * D, generator=g).half()
+    q, kt, v = O.qkv_split_heads_ref(qkv, Hn, bias)
+    full = (qkv.float() + bias.float()).half()
+    for b in range(B):
+        for i in range(Hn):
+            for t in range(S):
+                for e in range(D):
+                    assert q[b * Hn + i, t, e] == full[b, t, i * D + e]
+                    assert kt[b * Hn + i, e, t] == full[b, t, Hn * D + i * D + e]
+                    assert v[b * Hn + i, t, e] == full[b, t, 2 * Hn * D + i * D + e]
+    assert torch.equal(O.merge_heads_ref(q, B), full[:, :, :Hn * D])
+    q0, _, _ = O.qkv_split_heads_ref(qkv, Hn)                        # no bias: a pure permutation
+    assert torch.equal(O.merge_heads_ref(q0, B), qkv[:, :, :Hn * D])
+
+
 def test_softmax_ref_matches_torch_and_invariants():
     g = torch.Generator().manual_seed(33)
     x = torch.randn(19, 781, generator=g)                    # the reference test's row length
