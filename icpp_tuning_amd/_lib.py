@@ -30,7 +30,7 @@ EXPORTED_SYMBOLS = (
     "icpp_workspace_bytes", "icpp_gemm", "icpp_gemm_bias_layernorm", "icpp_conv2d_nhwc", "icpp_conv2d_nhwc_fused",
     "icpp_layernorm_fwd", "icpp_layernorm_bwd_workspace_bytes", "icpp_layernorm_bwd", "icpp_softmax",
     "icpp_softmax_scaled_masked",
-    "icpp_gemm_bias_residual_layernorm", "icpp_qkv_split_heads", "icpp_merge_heads",
+    "icpp_gemm_bias_residual_layernorm", "icpp_qkv_split_heads", "icpp_merge_heads", "icpp_attention_fwd",
 )
 CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
@@ -74,7 +74,8 @@ _SIGNATURES = {
     "icpp_layernorm_bwd": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "icpp_softmax": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "icpp_softmax_scaled_masked": (_i, [_i, _vp, _vp, _vp, _f, _i, _i, _i, _i, _i, _vp]),
-    "icpp_qkv_split_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "icpp_qkv_split_heads": (_i, [_i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "icpp_attention_fwd": (_i, [_i, _vp, _vp, _vp, _vp, _f, _vp, _i, _i, _i, _i, _vp]),
     "icpp_merge_heads": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
 }
 

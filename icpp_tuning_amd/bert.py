@@ -71,16 +71,24 @@ class BertLayerWeights:
         return BertLayerWeights(*[getattr(self, f).to(device) for f in self.__dataclass_fields__])
 
 
+# Longest sequence sent to the fused attention kernel.  Each of its waves streams the
+# whole K and V^T of its head from L2; measured against the batched-product path
+# (split, bmm, scaled masked softmax, bmm, merge), b x s = 32x128 / 16x256 / 8x384 /
+# 8x512: 30.5 / 45.9 / 69.3 / 93.4 us fused against 59.5 / 60.4 / 83.6 / 87.9 us.
+ATTENTION_FUSED_MAX_SEQ = 384
+
+
 def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch.Tensor,
                    softmax=None, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """softmax(q k^T / sqrt(d) + mask) v over heads, [b, s, 3H] -> [b, s, H] (end2end.py:47-71),
     with q, k, v taken from qkv (+ bias, [3H], when given).
 
-    Default path: icpp_qkv_split_heads writes q, k^T and v per head with the bias added
-    (head_size 64; other sizes use one strided add into [3, b, h, s, d] and a k copy), the
-    scores come from one batched product, icpp_softmax_scaled_masked applies the scale,
-    the additive mask and the softmax in one pass, and icpp_merge_heads lays the context
-    back out as [b, s, H].  With ``softmax`` given (a row softmax),
+    Default path: icpp_qkv_split_heads writes q, k and v per head with the bias added,
+    then icpp_attention_fwd computes softmax(q k^T / sqrt(d) + mask) v in one launch and
+    writes [b, s, H] (head_size 64, seq a multiple of 32 up to ATTENTION_FUSED_MAX_SEQ).  Other sequence
+    lengths: k^T from the split, the scores from one batched product,
+    icpp_softmax_scaled_masked (scale, additive mask and softmax in one pass), and
+    icpp_merge_heads; other head sizes: one strided add into [3, b, h, s, d] and a k copy.  With ``softmax`` given (a row softmax),
     the reference's order is kept op for op -- scale, mask add, softmax -- as the torch
     composition this layer is measured against."""
     b, s, _ = qkv.shape
@@ -97,6 +105,10 @@ def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch
         attn = softmax(scores.contiguous()).view(b * head_num, s, s)
     else:
         fused = head_size == runtime.HEAD_DIM and qkv.dtype in (torch.float16, torch.bfloat16)
+        if fused and s % 32 == 0 and s <= ATTENTION_FUSED_MAX_SEQ:
+            # one kernel for the scores, the scaled masked softmax and P V (K, V^T per head)
+            q, k, vt = runtime.qkv_split_heads(qkv.contiguous(), head_num, bias, layout=1)
+            return runtime.attention_fwd(q, k, vt, b, 1.0 / math.sqrt(head_size), mask.to(qkv.dtype).contiguous())
         if fused:
             q, k, v = runtime.qkv_split_heads(qkv.contiguous(), head_num, bias)   # k: [b*h, d, s]
         else:
@@ -160,4 +172,4 @@ def bert_forward(layers: List[BertLayer], input_from_tensor: torch.Tensor, qkv_k
     return hidden
 
 
-__all__ = ["BertLayer", "BertLayerWeights", "attention_core", "bert_forward", "causal_mask", "transpose_for_scores"]
+__all__ = ["ATTENTION_FUSED_MAX_SEQ", "BertLayer", "BertLayerWeights", "attention_core", "bert_forward", "causal_mask", "transpose_for_scores"]

@@ -522,19 +522,22 @@ layernorm_dwdb_kernel(const float* __restrict__ part, T* __restrict__ DW, T* __r
 // Attention head layout (BERT attention core, head_dim 64)
 // ---------------------------------------------------------------------------
 // qkv_split_heads: the fused QKV projection [T = batch*seq, 3*H] (H = heads*64) plus
-// its bias [3H] -> Q [batch, heads, seq, 64], K^T [batch, heads, 64, seq] and
-// V [batch, heads, seq, 64].  A workgroup takes 64 rows of one (batch, head): it
+// its bias [3H] -> Q [batch, heads, seq, 64] and K, V per head, one of them
+// transposed: TP = 1 gives K^T [batch, heads, 64, seq] and V [.., seq, 64] (the
+// batched-product attention), TP = 2 gives K [.., seq, 64] and V^T [.., 64, seq]
+// (the fused attention kernel).  A workgroup takes 64 rows of one (batch, head): it
 // reads three 64 x 64 blocks (one 128-byte row segment per token), adds the bias
-// in fp32 and rounds once (as torch's add of two 16-bit tensors), writes Q and V
-// as contiguous 8 KiB blocks and K through a padded LDS tile (row stride 66
-// elements, so a column read spreads over the banks) as 64 rows of 64 tokens.
-// Every access is a 16-byte chunk; rows past seq are neither read nor written.
+// in fp32 and rounds once (as torch's add of two 16-bit tensors), writes the
+// untransposed parts as contiguous 8 KiB blocks and part TP through a padded LDS
+// tile (row stride 66 elements, so a column read spreads over the banks) as 64
+// rows of 64 tokens.  Every access is a 16-byte chunk; rows past seq are neither
+// read nor written.
 constexpr int HD = 64;            // head_dim this kernel serves
 constexpr int KT_LD = HD + 2;     // LDS tile row stride (elements)
-template <typename T>
+template <typename T, int TP>
 __global__ void __launch_bounds__(256)
 qkv_split_heads_kernel(const T* __restrict__ QKV, const T* __restrict__ bias, T* __restrict__ Q,
-                       T* __restrict__ KT, T* __restrict__ V, int seq, int heads) {
+                       T* __restrict__ K, T* __restrict__ V, int seq, int heads) {
   __shared__ T kt[HD][KT_LD];
   const int s0 = blockIdx.x * HD, hh = blockIdx.y, bb = blockIdx.z;
   const int H = heads * HD;
@@ -557,23 +560,23 @@ qkv_split_heads_kernel(const T* __restrict__ QKV, const T* __restrict__ bias, T*
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] += bv[e];
       }
-      if (part == 1) {
+      if (part == TP) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) kt[c * 8 + e][r] = from_f<T>(v[e]);
       } else {
-        store_chunk<T, 8>((part == 0 ? Q : V) + (bh * seq + ss) * HD + c * 8, v);
+        store_chunk<T, 8>((part == 0 ? Q : part == 1 ? K : V) + (bh * seq + ss) * HD + c * 8, v);
       }
     }
   }
   __syncthreads();
-  // K^T rows: head dim d, 64 tokens s0 .. s0+63 (8 chunks of 8 tokens)
+  // rows of the transposed part: head dim d, 64 tokens s0 .. s0+63 (8 chunks of 8 tokens)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int q = threadIdx.x + 256 * i;
     const int d = q >> 3, c = q & 7;
     const int ss = s0 + c * 8;
     if (ss >= seq) continue;
-    T* out = KT + (bh * HD + d) * (size_t)seq + ss;
+    T* out = (TP == 1 ? K : V) + (bh * HD + d) * (size_t)seq + ss;
     if (ss + 8 <= seq && (seq & 7) == 0) {
       float v[8];
 #pragma unroll
@@ -836,24 +839,31 @@ int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* ma
 }
 
 // Attention head layout (head_dim 64): see qkv_split_heads_kernel / merge_heads_kernel.
-int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* KT, void* V, int batch,
-                         int seq, int heads, int head_dim, void* stream) {
-  if (!QKV || !Q || !KT || !V) return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: null tensor");
+int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* K, void* V, int batch,
+                         int seq, int heads, int head_dim, int layout, void* stream) {
+  if (!QKV || !Q || !K || !V) return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: null tensor");
+  if (layout != 0 && layout != 1) return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: layout must be 0 or 1");
   if (dtype != ICPP_F16 && dtype != ICPP_BF16) return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: dtype must be f16 or bf16");
   if (head_dim != HD) return set_error(ICPP_E_SHAPE, "icpp_qkv_split_heads: head_dim must be 64");
   if (batch <= 0 || seq <= 0 || heads <= 0 || (long long)batch * seq * heads * 3 * HD > 0x7FFFFFFFll)
     return set_error(ICPP_E_SHAPE, "icpp_qkv_split_heads: bad or too large shape");
-  if (!aligned16(QKV) || (bias && !aligned16(bias)) || !aligned16(Q) || !aligned16(KT) || !aligned16(V))
+  if (!aligned16(QKV) || (bias && !aligned16(bias)) || !aligned16(Q) || !aligned16(K) || !aligned16(V))
     return set_error(ICPP_E_ARG, "icpp_qkv_split_heads: pointers must be 16-byte aligned");
   const dim3 grid((seq + HD - 1) / HD, heads, batch);
   if (batch > 65535 || heads > 65535) return set_error(ICPP_E_SHAPE, "icpp_qkv_split_heads: grid too large");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == ICPP_F16)
-    hipLaunchKernelGGL(qkv_split_heads_kernel<_Float16>, grid, dim3(256), 0, s, (const _Float16*)QKV,
-                       (const _Float16*)bias, (_Float16*)Q, (_Float16*)KT, (_Float16*)V, seq, heads);
-  else
-    hipLaunchKernelGGL(qkv_split_heads_kernel<__bf16>, grid, dim3(256), 0, s, (const __bf16*)QKV,
-                       (const __bf16*)bias, (__bf16*)Q, (__bf16*)KT, (__bf16*)V, seq, heads);
+  auto launch = [&](auto tag, auto TPc) {
+    typedef decltype(tag) T;
+    hipLaunchKernelGGL((qkv_split_heads_kernel<T, decltype(TPc)::value>), grid, dim3(256), 0, s, (const T*)QKV,
+                       (const T*)bias, (T*)Q, (T*)K, (T*)V, seq, heads);
+  };
+  if (dtype == ICPP_F16) {
+    if (layout == 0) launch(_Float16{}, std::integral_constant<int, 1>{});
+    else launch(_Float16{}, std::integral_constant<int, 2>{});
+  } else {
+    if (layout == 0) launch(__bf16{}, std::integral_constant<int, 1>{});
+    else launch(__bf16{}, std::integral_constant<int, 2>{});
+  }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
 }

@@ -242,10 +242,11 @@ def softmax_scaled_masked(x: torch.Tensor, scale: float, mask: Optional[torch.Te
 HEAD_DIM = 64  # head size the attention layout kernels serve
 
 
-def qkv_split_heads(qkv: torch.Tensor, heads: int, bias: Optional[torch.Tensor] = None):
-    """[batch, seq, 3*heads*64] (+ bias [3*heads*64]) -> (q [batch*heads, seq, 64],
-    k^T [batch*heads, 64, seq], v [batch*heads, seq, 64]) through icpp_qkv_split_heads
-    (end2end.py:48-58: qkv + bias, chunk, transpose_for_scores, permute, k rearranged)."""
+def qkv_split_heads(qkv: torch.Tensor, heads: int, bias: Optional[torch.Tensor] = None, layout: int = 0):
+    """[batch, seq, 3*heads*64] (+ bias [3*heads*64]) -> per head, through icpp_qkv_split_heads
+    (end2end.py:48-58: qkv + bias, chunk, transpose_for_scores, permute, k rearranged):
+    layout 0: (q [b*h, seq, 64], k^T [b*h, 64, seq], v [b*h, seq, 64]);
+    layout 1: (q, k [b*h, seq, 64], v^T [b*h, 64, seq]) for attention_fwd."""
     if qkv.dim() != 3 or qkv.dtype not in (torch.float16, torch.bfloat16) or not qkv.is_contiguous():
         raise ValueError("qkv_split_heads: qkv must be a contiguous [batch, seq, 3H] f16 / bf16 tensor")
     b, s, w = qkv.shape
@@ -254,12 +255,32 @@ def qkv_split_heads(qkv: torch.Tensor, heads: int, bias: Optional[torch.Tensor] 
     if bias is not None and (bias.dtype != qkv.dtype or not bias.is_contiguous() or bias.numel() != w):
         raise ValueError("qkv_split_heads: bias must be a contiguous [3H] tensor of qkv's dtype")
     q = torch.empty((b * heads, s, HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
-    kt = torch.empty((b * heads, HEAD_DIM, s), dtype=qkv.dtype, device=qkv.device)
-    v = torch.empty_like(q)
+    t = torch.empty((b * heads, HEAD_DIM, s), dtype=qkv.dtype, device=qkv.device)
+    u = torch.empty_like(q)
+    k, v = (t, u) if layout == 0 else (u, t)
     lib().call("icpp_qkv_split_heads", DTYPE[ROW_DTYPE[qkv.dtype]], qkv.data_ptr(),
-               bias.data_ptr() if bias is not None else None, q.data_ptr(), kt.data_ptr(), v.data_ptr(),
-               b, s, heads, HEAD_DIM, _stream())
-    return q, kt, v
+               bias.data_ptr() if bias is not None else None, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+               b, s, heads, HEAD_DIM, int(layout), _stream())
+    return q, k, v
+
+
+def attention_fwd(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, batch: int, scale: float,
+                  mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """softmax(q k^T * scale + mask) v per (batch, head) -> [batch, seq, heads*64] through
+    icpp_attention_fwd (end2end.py:59-71).  q, k [b*h, seq, 64], vt [b*h, 64, seq]
+    (qkv_split_heads layout 1); mask [seq, seq] in q's dtype or None."""
+    bh, s, d = q.shape
+    if d != HEAD_DIM or k.shape != q.shape or vt.shape != (bh, d, s) or bh % batch \
+            or any(not t.is_contiguous() or t.dtype != q.dtype for t in (q, k, vt)):
+        raise ValueError("attention_fwd: q, k [b*h, s, 64] and vt [b*h, 64, s], contiguous, one dtype")
+    if mask is not None and (mask.shape != (s, s) or mask.dtype != q.dtype or not mask.is_contiguous()):
+        raise ValueError("attention_fwd: mask must be a contiguous [seq, seq] tensor of q's dtype")
+    heads = bh // batch
+    o = torch.empty((batch, s, heads * HEAD_DIM), dtype=q.dtype, device=q.device)
+    lib().call("icpp_attention_fwd", DTYPE[ROW_DTYPE[q.dtype]], q.data_ptr(), k.data_ptr(), vt.data_ptr(),
+               mask.data_ptr() if mask is not None else None, float(scale), o.data_ptr(), batch, s, heads,
+               HEAD_DIM, _stream())
+    return o
 
 
 def merge_heads(ctx: torch.Tensor, batch: int) -> torch.Tensor:
@@ -275,5 +296,5 @@ def merge_heads(ctx: torch.Tensor, batch: int) -> torch.Tensor:
 
 
 __all__ = ["BIAS_DTYPE", "HEAD_DIM", "OUT_DTYPE", "ROW_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
-           "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "merge_heads", "qkv_split_heads", "softmax",
+           "attention_fwd", "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "merge_heads", "qkv_split_heads", "softmax",
            "softmax_scaled_masked", "workspace_bytes"]

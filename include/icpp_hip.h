@@ -211,15 +211,29 @@ int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* ma
  * icpp_qkv_split_heads replaces `qkv + qkv_bias`, `chunk(3)`, transpose_for_scores
  * and the three permute(0, 2, 1, 3).contiguous() copies plus the k rearrange to
  * [(b h), d, s] (evaluation/end2end.py:48-58): QKV [batch*seq, 3*heads*64] row-major
- * (+ bias [3*heads*64], or null) -> Q and V [batch, heads, seq, 64], KT
- * [batch, heads, 64, seq]; the bias add is one fp32 add rounded to the dtype.
+ * (+ bias [3*heads*64], or null) -> Q [batch, heads, seq, 64] and, with layout 0,
+ * K^T [batch, heads, 64, seq] in K and V [batch, heads, seq, 64]; with layout 1,
+ * K [batch, heads, seq, 64] and V^T [batch, heads, 64, seq] (icpp_attention_fwd's
+ * operands).  The bias add is one fp32 add rounded to the dtype.
  * icpp_merge_heads replaces the context reshape back to [batch*seq, heads*64]
  * (end2end.py:68-71): X [batch, heads, seq, 64] -> Y [batch*seq, heads*64].
  * Pointers 16-byte aligned; batch*seq*heads*3*64 below 2^31.
  */
-int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* KT, void* V, int batch,
-                         int seq, int heads, int head_dim, void* stream);
+int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* K, void* V, int batch,
+                         int seq, int heads, int head_dim, int layout, void* stream);
 int icpp_merge_heads(int dtype, const void* X, void* Y, int batch, int seq, int heads, int head_dim, void* stream);
+
+/*
+ * Fused attention of the reference's BERT layer (evaluation/end2end.py:59-71:
+ * baddbmm(q, k) * 1/sqrt(d) + causal mask, softmax, einsum with v, reshape to
+ * [b, t, h*d]): O [batch*seq, heads*64] = softmax(Q K^T * scale + mask) V per
+ * (batch, head), from Q and K [batch, heads, seq, 64] and VT [batch, heads, 64, seq]
+ * (icpp_qkv_split_heads layout 1).  mask is [seq, seq] in the data type, or null.
+ * Scores and softmax in fp32; P is rounded to the data type before P V.
+ * f16 / bf16, head_dim 64, seq a multiple of 32 up to 512.
+ */
+int icpp_attention_fwd(int dtype, const void* Q, const void* K, const void* VT, const void* mask, float scale, void* O,
+                       int batch, int seq, int heads, int head_dim, void* stream);
 
 #ifdef __cplusplus
 }

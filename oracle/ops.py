@@ -156,6 +156,17 @@ def qkv_split_heads_ref(qkv, heads: int, bias=None):
     return per_head[0], per_head[1].transpose(1, 2).contiguous(), per_head[2]
 
 
+def attention_ref(q, k, v, batch: int, scale: float, mask=None):
+    """softmax(q k^T * scale + mask) v per (batch, head) in fp32 on the CPU, merged to
+    [batch, seq, heads*d] (end2end.py:59-71).  q, k, v [batch*heads, seq, d]; mask [seq, seq]."""
+    qf, kf, vf = q.float().cpu(), k.float().cpu(), v.float().cpu()
+    z = torch.bmm(qf, kf.transpose(1, 2)) * scale
+    if mask is not None:
+        z = z + mask.float().cpu()
+    p = torch.softmax(z, dim=-1)
+    return merge_heads_ref(torch.bmm(p, vf), batch)
+
+
 def merge_heads_ref(ctx, batch: int):
     """[batch*heads, s, d] -> [batch, s, heads*d] (end2end.py:68-71: the context's
     'b h t d -> b t (h d)' reshape), on the CPU."""

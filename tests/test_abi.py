@@ -139,11 +139,19 @@ def test_rowops_validation_errors_before_launch(L):
     assert smm(f32, 16, 16, None, float("inf"), 4, 64, 64, 64, 1, None) == -4          # non-finite scale
     assert smm(f32, 16, 16, None, float("nan"), 4, 64, 64, 64, 1, None) == -4
     qs, mh = L._dll.icpp_qkv_split_heads, L._dll.icpp_merge_heads
-    assert qs(f16, None, None, 16, 16, 16, 2, 128, 12, 64, None) == -4                 # null qkv
-    assert qs(f16, 16, None, 16, 16, 16, 2, 128, 12, 32, None) == -2                   # head_dim 64 only
-    assert qs(f32, 16, None, 16, 16, 16, 2, 128, 12, 64, None) == -4                   # f16 / bf16 only
-    assert qs(f16, 24, None, 16, 16, 16, 2, 128, 12, 64, None) == -4                   # misaligned
-    assert qs(f16, 16, None, 16, 16, 16, 0, 128, 12, 64, None) == -2                   # empty
+    assert qs(f16, None, None, 16, 16, 16, 2, 128, 12, 64, 0, None) == -4              # null qkv
+    assert qs(f16, 16, None, 16, 16, 16, 2, 128, 12, 32, 0, None) == -2                # head_dim 64 only
+    assert qs(f32, 16, None, 16, 16, 16, 2, 128, 12, 64, 0, None) == -4                # f16 / bf16 only
+    assert qs(f16, 24, None, 16, 16, 16, 2, 128, 12, 64, 0, None) == -4                # misaligned
+    assert qs(f16, 16, None, 16, 16, 16, 0, 128, 12, 64, 0, None) == -2                # empty
+    assert qs(f16, 16, None, 16, 16, 16, 2, 128, 12, 64, 2, None) == -4                # layout 0 or 1
+    att = L._dll.icpp_attention_fwd
+    assert att(f16, 16, 16, 16, None, 0.125, 16, 2, 100, 12, 64, None) == -2           # seq % 32
+    assert att(f16, 16, 16, 16, None, 0.125, 16, 2, 544, 12, 64, None) == -2           # seq <= 512
+    assert att(f16, 16, 16, 16, None, float("inf"), 16, 2, 128, 12, 64, None) == -4
+    assert att(f16, None, 16, 16, None, 0.125, 16, 2, 128, 12, 64, None) == -4
+    assert att(f16, 16, 16, 16, 24, 0.125, 16, 2, 128, 12, 64, None) == -4             # misaligned mask
+    assert "icpp_attention_fwd" in L.last_error()
     assert mh(f16, 16, 16, 2, 128, 12, 48, None) == -2
     assert mh(f16, 16, None, 2, 128, 12, 64, None) == -4
     assert "icpp_merge_heads" in L.last_error()

@@ -191,7 +191,34 @@ def test_qkv_split_and_merge_heads(gpu, dtype, b, s, heads, with_bias):
     torch.cuda.synchronize()
     for name, w, o in zip(("q", "k^T", "v"), want, got):
         assert torch.equal(o.cpu().view(torch.int16), w.view(torch.int16)), name
+    # layout 1: k untransposed, v transposed
+    got1 = runtime.qkv_split_heads(qkv.cuda(), heads, bias.cuda() if bias is not None else None, layout=1)
+    torch.cuda.synchronize()
+    want1 = (want[0], want[1].transpose(1, 2).contiguous(), want[2].transpose(1, 2).contiguous())
+    for name, w, o in zip(("q", "k", "v^T"), want1, got1):
+        assert torch.equal(o.cpu().view(torch.int16), w.view(torch.int16)), name
     ctx = (torch.rand(b * heads, s, 64, generator=g) - 0.5).to(dtype)
     y = runtime.merge_heads(ctx.cuda(), b)
     torch.cuda.synchronize()
     assert torch.equal(y.cpu().view(torch.int16), O.merge_heads_ref(ctx, b).view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b,s,heads,masked", [(2, 128, 12, True), (1, 32, 3, True), (3, 96, 2, False),
+                                               (1, 512, 2, True), (2, 288, 1, True)])
+def test_attention_fwd(gpu, dtype, b, s, heads, masked):
+    """icpp_attention_fwd against fp32 attention on the CPU: the BERT layer's causal mask
+    (-10000 above the diagonal), sequence lengths in each of the kernel's three register
+    buckets (<= 128, <= 256, <= 512), a partial last 64-query block (96, 288) and no mask.
+    Tolerance 1e-2 + 1e-2 |ref| (P is rounded to the data type before P V)."""
+    g = torch.Generator().manual_seed(b * 7 + s + heads)
+    q = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
+    k = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
+    v = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
+    mask = torch.triu(torch.full((s, s), -10000.0), 1).to(dtype) if masked else None
+    want = O.attention_ref(q, k, v, b, 0.125, mask)
+    print(f"[parity] attention_fwd b={b} s={s} heads={heads} {dtype} masked={masked}", flush=True)
+    got = runtime.attention_fwd(q.cuda(), k.cuda(), v.transpose(1, 2).contiguous().cuda(), b, 0.125,
+                                mask.cuda() if mask is not None else None)
+    torch.cuda.synchronize()
+    _close(got.float().cpu(), want, 1e-2, 1e-2, f"attention b={b} s={s} {dtype}")
