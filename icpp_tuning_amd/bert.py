@@ -71,11 +71,11 @@ class BertLayerWeights:
         return BertLayerWeights(*[getattr(self, f).to(device) for f in self.__dataclass_fields__])
 
 
-# Longest sequence sent to the fused attention kernel.  Each of its waves streams the
-# whole K and V^T of its head from L2; measured against the batched-product path
-# (split, bmm, scaled masked softmax, bmm, merge), b x s = 32x128 / 16x256 / 8x384 /
-# 8x512: 30.5 / 45.9 / 69.3 / 93.4 us fused against 59.5 / 60.4 / 83.6 / 87.9 us.
-ATTENTION_FUSED_MAX_SEQ = 384
+# Longest sequence sent to the fused attention kernel (its limit).  Measured against the
+# batched-product path (split, bmm, scaled masked softmax, bmm, merge), b x s = 32x128 /
+# 16x256 / 8x384 / 8x512: 30.4 / 46.1 / 63.9 / 84.9 us fused against 59.5 / 59.8 / 83.2 /
+# 87.9 us.
+ATTENTION_FUSED_MAX_SEQ = 512
 
 
 def attention_core(qkv: torch.Tensor, head_num: int, head_size: int, mask: torch.Tensor,

@@ -4,8 +4,9 @@
 // einsum with v, reshaped to [b, t, h*d]), one launch instead of two batched
 // products, a softmax pass and the context merge.
 //
-// A wave owns 16 queries of one (batch, head); four waves share a workgroup but
-// never synchronise with each other.  Per wave:
+// A wave owns 16 queries of one (batch, head).  Up to 256 keys the four waves of
+// a workgroup never synchronise; longer sequences use a variant that shares K and
+// V^T through LDS (below).  Per wave:
 //   1. S = Q K^T for all keys with 16x16x32 MFMAs: the 16 x 64 query block stays
 //      in two fragments, every 16-key tile of K [seq, 64] is read straight from
 //      global memory (16 contiguous bytes per lane).  S stays in registers (up to
@@ -149,6 +150,166 @@ attention_fwd_kernel(const void* Qp, const void* Kp, const void* VTp, const void
   }
 }
 
+// Long sequences (up to 512 keys): the same per-wave work, but the four waves share
+// K and V^T through LDS in chunks of 128 keys (each loaded once per workgroup instead
+// of once per wave), with two workgroup barriers per chunk.  Every wave takes part in
+// the loads and barriers; a wave past the last query only skips the arithmetic.
+constexpr int CH = 128;          // keys per chunk
+constexpr int KST = AD + 8;      // K chunk row stride (elements): 16 key rows of a fragment read hit distinct banks
+constexpr int VST = CH + 8;      // V^T chunk row stride (elements)
+template <int DT>
+__global__ void __launch_bounds__(256)
+attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, const void* Mp, void* Op, int seq,
+                            int heads, float scale) {
+  typedef typename DTraits<DT>::T T;
+  typedef Mfma<DT, 16> MF;
+  typedef T t4 __attribute__((ext_vector_type(4)));
+  constexpr int NT_MAX = ATT_MAX_SEQ / 16, NC = ATT_MAX_SEQ / CH, PST_MAX = ATT_MAX_SEQ + 8;
+  __shared__ __attribute__((aligned(16))) T plds[4][16 * PST_MAX];
+  __shared__ __attribute__((aligned(16))) T kv[CH * KST > AD * VST ? CH * KST : AD * VST];
+  const T* Q = (const T*)Qp;
+  const T* K = (const T*)Kp;
+  const T* VT = (const T*)VTp;
+  const T* M = (const T*)Mp;
+  T* O = (T*)Op;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int bh = blockIdx.y;
+  const int bb = bh / heads, hh = bh - bb * heads;
+  const int q0 = blockIdx.x * 64 + wave * 16;
+  const bool active = q0 < seq;
+  const int NT = seq / 16;
+  const int PST = seq + 8;
+  const int q = q0 + r;
+  const bool qok = q < seq;
+
+  i32x4 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    qf[ks] = qok ? *reinterpret_cast<const i32x4*>(Q + ((size_t)bh * seq + q) * AD + ks * 32 + g * 8)
+                 : i32x4{0, 0, 0, 0};
+
+  float sv[NT_MAX][4];
+#pragma unroll
+  for (int kt = 0; kt < NT_MAX; ++kt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sv[kt][j] = -INFINITY;
+  // 1. scores, one 128-key chunk of K at a time: 128 rows x 8 chunks of 16 bytes, 4 per thread
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c * CH < seq) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int x = tid + 256 * i;
+        const int kr = x >> 3, kc = x & 7;
+        const int key = c * CH + kr;
+        if (key < seq)
+          *reinterpret_cast<i32x4*>(kv + kr * KST + kc * 8) =
+              *reinterpret_cast<const i32x4*>(K + ((size_t)bh * seq + key) * AD + kc * 8);
+      }
+      __syncthreads();
+      if (active) {
+#pragma unroll
+        for (int t = 0; t < CH / 16; ++t) {
+          const int kt = c * (CH / 16) + t;
+          if (kt < NT) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              const i32x4 kf = *reinterpret_cast<const i32x4*>(kv + (t * 16 + r) * KST + ks * 32 + g * 8);
+              acc = MF::run(kf, qf[ks], acc);
+            }
+            f32x4 mk = {0.f, 0.f, 0.f, 0.f};
+            if (M != nullptr && qok) {
+              const t4 m4 = *reinterpret_cast<const t4*>(M + (size_t)q * seq + kt * 16 + 4 * g);
+              mk = f32x4{(float)m4[0], (float)m4[1], (float)m4[2], (float)m4[3]};
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sv[kt][j] = fmaf(acc[j], scale, mk[j]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // 2. row softmax
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < NT_MAX; ++kt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, sv[kt][j]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  float sum = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < NT_MAX; ++kt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e = kt < NT ? __expf(sv[kt][j] - mx) : 0.f;
+      sv[kt][j] = e;
+      sum += e;
+    }
+  sum += __shfl_xor(sum, 16);
+  sum += __shfl_xor(sum, 32);
+  const float inv = 1.f / sum;
+  T* prow = plds[wave];
+#pragma unroll
+  for (int kt = 0; kt < NT_MAX; ++kt)
+    if (kt < NT) {
+      const t4 pv = {(T)(sv[kt][0] * inv), (T)(sv[kt][1] * inv), (T)(sv[kt][2] * inv), (T)(sv[kt][3] * inv)};
+      *reinterpret_cast<t4*>(prow + r * PST + kt * 16 + 4 * g) = pv;
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // 3. O = P V, one 128-key chunk of V^T at a time: 64 rows x 16 chunks of 16 bytes, 4 per thread
+  f32x4 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c * CH < seq) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int x = tid + 256 * i;
+        const int d = x >> 4, kc = x & 15;
+        const int key = c * CH + kc * 8;
+        if (key < seq)
+          *reinterpret_cast<i32x4*>(kv + d * VST + kc * 8) =
+              *reinterpret_cast<const i32x4*>(VT + ((size_t)bh * AD + d) * seq + key);
+      }
+      __syncthreads();
+      if (active) {
+#pragma unroll
+        for (int u = 0; u < CH / 32; ++u) {
+          const int kk = c * (CH / 32) + u;
+          if (2 * kk < NT) {
+            const i32x4 pf = *reinterpret_cast<const i32x4*>(prow + r * PST + kk * 32 + g * 8);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+              const i32x4 vf = *reinterpret_cast<const i32x4*>(kv + (dt * 16 + r) * VST + u * 32 + g * 8);
+              oacc[dt] = MF::run(vf, pf, oacc[dt]);
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  if (qok) {
+    T* orow = O + ((size_t)bb * seq + q) * ((size_t)heads * AD) + hh * AD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const t4 ov = {(T)oacc[dt][0], (T)oacc[dt][1], (T)oacc[dt][2], (T)oacc[dt][3]};
+      *reinterpret_cast<t4*>(orow + dt * 16 + 4 * g) = ov;
+    }
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <int DT>
@@ -160,7 +321,7 @@ hipError_t launch_attention(const void* Q, const void* K, const void* VT, const 
   else if (seq <= 256)
     hipLaunchKernelGGL((attention_fwd_kernel<DT, 16>), grid, dim3(256), 0, s, Q, K, VT, M, O, seq, heads, scale);
   else
-    hipLaunchKernelGGL((attention_fwd_kernel<DT, 32>), grid, dim3(256), 0, s, Q, K, VT, M, O, seq, heads, scale);
+    hipLaunchKernelGGL((attention_fwd_staged_kernel<DT>), grid, dim3(256), 0, s, Q, K, VT, M, O, seq, heads, scale);
   return hipGetLastError();
 }
 

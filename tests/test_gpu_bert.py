@@ -74,8 +74,8 @@ def test_gemm_bias_gelu_erf(gpu):
     assert (y.float().cpu() - ref).abs().mean() < (tanh_ref - ref).abs().mean()
 
 
-# (1, 128) and (4, 64): the fused attention kernel; (1, 416): past ATTENTION_FUSED_MAX_SEQ,
-# the batched-product path; (2, 40): a length off the 32-key step, the same path
+# (1, 128) and (4, 64): the fused attention kernel; (1, 416): its LDS-staged variant (over
+# 256 keys); (2, 40): a length off the 32-key step, the batched-product path
 @pytest.mark.parametrize("batch,seq,layers", [(1, 128, 2), (4, 64, 1), (1, 416, 1), (2, 40, 1)])
 def test_bert_layers(gpu, batch, seq, layers):
     heads, hsize = 12, 64
