@@ -1,6 +1,6 @@
 // Fused attention forward of the BERT layer, head_dim 64:
 //   O[b, s, h*64] = softmax(Q K^T * scale + mask) V   per (batch, head)
-// (evaluation/end2end.py:59-71: baddbmm(q, k) * 1/sqrt(d), + causal mask, softmax,
+// (evaluation/end2end.py:59-73: baddbmm(q, k) * 1/sqrt(d), + causal mask, softmax,
 // einsum with v, reshaped to [b, t, h*d]), one launch instead of two batched
 // products, a softmax pass and the context merge.
 //

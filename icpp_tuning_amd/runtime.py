@@ -267,7 +267,7 @@ def qkv_split_heads(qkv: torch.Tensor, heads: int, bias: Optional[torch.Tensor] 
 def attention_fwd(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, batch: int, scale: float,
                   mask: Optional[torch.Tensor] = None) -> torch.Tensor:
     """softmax(q k^T * scale + mask) v per (batch, head) -> [batch, seq, heads*64] through
-    icpp_attention_fwd (end2end.py:59-71).  q, k [b*h, seq, 64], vt [b*h, 64, seq]
+    icpp_attention_fwd (end2end.py:59-73).  q, k [b*h, seq, 64], vt [b*h, 64, seq]
     (qkv_split_heads layout 1); mask [seq, seq] in q's dtype or None."""
     bh, s, d = q.shape
     if d != HEAD_DIM or k.shape != q.shape or vt.shape != (bh, d, s) or bh % batch \
@@ -284,7 +284,7 @@ def attention_fwd(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, batch: int
 
 
 def merge_heads(ctx: torch.Tensor, batch: int) -> torch.Tensor:
-    """[batch*heads, seq, 64] -> [batch, seq, heads*64] through icpp_merge_heads (end2end.py:68-71)."""
+    """[batch*heads, seq, 64] -> [batch, seq, heads*64] through icpp_merge_heads (end2end.py:72-73)."""
     if ctx.dim() != 3 or ctx.shape[2] != HEAD_DIM or ctx.dtype not in (torch.float16, torch.bfloat16) \
             or not ctx.is_contiguous() or ctx.shape[0] % batch:
         raise ValueError("merge_heads: ctx must be a contiguous [batch*heads, seq, 64] f16 / bf16 tensor")

@@ -216,7 +216,7 @@ int icpp_softmax_scaled_masked(int dtype, const void* X, void* Y, const void* ma
  * K [batch, heads, seq, 64] and V^T [batch, heads, 64, seq] (icpp_attention_fwd's
  * operands).  The bias add is one fp32 add rounded to the dtype.
  * icpp_merge_heads replaces the context reshape back to [batch*seq, heads*64]
- * (end2end.py:68-71): X [batch, heads, seq, 64] -> Y [batch*seq, heads*64].
+ * (end2end.py:72-73): X [batch, heads, seq, 64] -> Y [batch*seq, heads*64].
  * Pointers 16-byte aligned; batch*seq*heads*3*64 below 2^31.
  */
 int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, void* K, void* V, int batch,
@@ -224,7 +224,7 @@ int icpp_qkv_split_heads(int dtype, const void* QKV, const void* bias, void* Q, 
 int icpp_merge_heads(int dtype, const void* X, void* Y, int batch, int seq, int heads, int head_dim, void* stream);
 
 /*
- * Fused attention of the reference's BERT layer (evaluation/end2end.py:59-71:
+ * Fused attention of the reference's BERT layer (evaluation/end2end.py:59-73:
  * baddbmm(q, k) * 1/sqrt(d) + causal mask, softmax, einsum with v, reshape to
  * [b, t, h*d]): O [batch*seq, heads*64] = softmax(Q K^T * scale + mask) V per
  * (batch, head), from Q and K [batch, heads, seq, 64] and VT [batch, heads, 64, seq]

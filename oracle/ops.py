@@ -158,7 +158,7 @@ def qkv_split_heads_ref(qkv, heads: int, bias=None):
 
 def attention_ref(q, k, v, batch: int, scale: float, mask=None):
     """softmax(q k^T * scale + mask) v per (batch, head) in fp32 on the CPU, merged to
-    [batch, seq, heads*d] (end2end.py:59-71).  q, k, v [batch*heads, seq, d]; mask [seq, seq]."""
+    [batch, seq, heads*d] (end2end.py:59-73).  q, k, v [batch*heads, seq, d]; mask [seq, seq]."""
     qf, kf, vf = q.float().cpu(), k.float().cpu(), v.float().cpu()
     z = torch.bmm(qf, kf.transpose(1, 2)) * scale
     if mask is not None:
@@ -168,7 +168,7 @@ def attention_ref(q, k, v, batch: int, scale: float, mask=None):
 
 
 def merge_heads_ref(ctx, batch: int):
-    """[batch*heads, s, d] -> [batch, s, heads*d] (end2end.py:68-71: the context's
+    """[batch*heads, s, d] -> [batch, s, heads*d] (end2end.py:72-73: the context's
     'b h t d -> b t (h d)' reshape), on the CPU."""
     x = ctx.cpu()
     bh, s, d = x.shape
