@@ -35,7 +35,7 @@ namespace {
 constexpr int AD = 64;        // head_dim
 constexpr int ATT_MAX_SEQ = 512;
 
-template <int DT, int NT_MAX>
+template <int DT, int NT_MAX, bool HAS_MASK>
 __global__ void __launch_bounds__(256)
 attention_fwd_kernel(const void* Qp, const void* Kp, const void* VTp, const void* Mp, void* Op, int seq, int heads,
                      float scale) {
@@ -67,27 +67,36 @@ attention_fwd_kernel(const void* Qp, const void* Kp, const void* VTp, const void
     qf[ks] = qok ? *reinterpret_cast<const i32x4*>(Q + ((size_t)bh * seq + q) * AD + ks * 32 + g * 8)
                  : i32x4{0, 0, 0, 0};
 
-  // 1. scores: lane holds S[q][kt*16 + 4g + j]
+  // 1. scores: lane holds S[q][kt*16 + 4g + j].  Every load is unconditional -- tiles
+  // past the last one re-read the last tile and rows past seq read row seq-1, results
+  // discarded -- so the unrolled loop has no branches and all K and mask loads can be
+  // in flight together instead of one round trip per tile.
+  const int qc = qok ? q : seq - 1;
   float sv[NT_MAX][4];
+  constexpr int KB = 8;  // key tiles whose loads are all issued before their MFMAs
 #pragma unroll
-  for (int kt = 0; kt < NT_MAX; ++kt) {
-    if (kt < NT) {
+  for (int kb = 0; kb < NT_MAX; kb += KB) {
+    i32x4 kf[KB][2];
+    t4 m4[KB];
+#pragma unroll
+    for (int t = 0; t < KB; ++t) {
+      const int kt = kb + t;
+      const int ktc = kt < NT ? kt : NT - 1;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        kf[t][ks] = *reinterpret_cast<const i32x4*>(K + ((size_t)bh * seq + ktc * 16 + r) * AD + ks * 32 + g * 8);
+      if constexpr (HAS_MASK) m4[t] = *reinterpret_cast<const t4*>(M + (size_t)qc * seq + ktc * 16 + 4 * g);
+    }
+#pragma unroll
+    for (int t = 0; t < KB; ++t) {
+      const int kt = kb + t;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const i32x4 kf = *reinterpret_cast<const i32x4*>(K + ((size_t)bh * seq + kt * 16 + r) * AD + ks * 32 + g * 8);
-        acc = MF::run(kf, qf[ks], acc);
-      }
+      for (int ks = 0; ks < 2; ++ks) acc = MF::run(kf[t][ks], qf[ks], acc);
       f32x4 mk = {0.f, 0.f, 0.f, 0.f};
-      if (M != nullptr && qok) {
-        const t4 m4 = *reinterpret_cast<const t4*>(M + (size_t)q * seq + kt * 16 + 4 * g);
-        mk = f32x4{(float)m4[0], (float)m4[1], (float)m4[2], (float)m4[3]};
-      }
+      if constexpr (HAS_MASK) mk = f32x4{(float)m4[t][0], (float)m4[t][1], (float)m4[t][2], (float)m4[t][3]};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sv[kt][j] = fmaf(acc[j], scale, mk[j]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sv[kt][j] = -INFINITY;
+      for (int j = 0; j < 4; ++j) sv[kt][j] = kt < NT ? fmaf(acc[j], scale, mk[j]) : -INFINITY;
     }
   }
 
@@ -126,16 +135,18 @@ attention_fwd_kernel(const void* Qp, const void* Kp, const void* VTp, const void
   f32x4 oacc[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // past the last 32-key step the V^T read is clamped and P is zero, so the MFMA adds nothing
 #pragma unroll
   for (int kk = 0; kk < NT_MAX / 2; ++kk) {
-    if (2 * kk < NT) {
-      const i32x4 pf = *reinterpret_cast<const i32x4*>(prow + r * PST + kk * 32 + g * 8);
+    const bool live = 2 * kk < NT;
+    const int kkc = live ? kk : NT / 2 - 1;
+    const i32x4 p_raw = *reinterpret_cast<const i32x4*>(prow + r * PST + kkc * 32 + g * 8);
+    const i32x4 pf = live ? p_raw : i32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const i32x4 vf =
-            *reinterpret_cast<const i32x4*>(VT + ((size_t)bh * AD + dt * 16 + r) * seq + kk * 32 + g * 8);
-        oacc[dt] = MF::run(vf, pf, oacc[dt]);
-      }
+    for (int dt = 0; dt < 4; ++dt) {
+      const i32x4 vf =
+          *reinterpret_cast<const i32x4*>(VT + ((size_t)bh * AD + dt * 16 + r) * seq + kkc * 32 + g * 8);
+      oacc[dt] = MF::run(vf, pf, oacc[dt]);
     }
   }
 
@@ -316,11 +327,17 @@ template <int DT>
 hipError_t launch_attention(const void* Q, const void* K, const void* VT, const void* M, void* O, int batch, int seq,
                             int heads, float scale, hipStream_t s) {
   const dim3 grid((seq + 63) / 64, batch * heads);
-  if (seq <= 128)
-    hipLaunchKernelGGL((attention_fwd_kernel<DT, 8>), grid, dim3(256), 0, s, Q, K, VT, M, O, seq, heads, scale);
-  else if (seq <= 256)
-    hipLaunchKernelGGL((attention_fwd_kernel<DT, 16>), grid, dim3(256), 0, s, Q, K, VT, M, O, seq, heads, scale);
-  else
+  auto direct = [&](auto NTc, auto MASKc) {
+    hipLaunchKernelGGL((attention_fwd_kernel<DT, decltype(NTc)::value, decltype(MASKc)::value>), grid, dim3(256), 0, s,
+                       Q, K, VT, M, O, seq, heads, scale);
+  };
+  if (seq <= 128) {
+    if (M) direct(std::integral_constant<int, 8>{}, std::true_type{});
+    else direct(std::integral_constant<int, 8>{}, std::false_type{});
+  } else if (seq <= 256) {
+    if (M) direct(std::integral_constant<int, 16>{}, std::true_type{});
+    else direct(std::integral_constant<int, 16>{}, std::false_type{});
+  } else
     hipLaunchKernelGGL((attention_fwd_staged_kernel<DT>), grid, dim3(256), 0, s, Q, K, VT, M, O, seq, heads, scale);
   return hipGetLastError();
 }
