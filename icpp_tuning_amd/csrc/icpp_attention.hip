@@ -175,8 +175,10 @@ attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, con
   typedef typename DTraits<DT>::T T;
   typedef Mfma<DT, 16> MF;
   typedef T t4 __attribute__((ext_vector_type(4)));
-  constexpr int NT_MAX = ATT_MAX_SEQ / 16, NC = ATT_MAX_SEQ / CH, PST_MAX = ATT_MAX_SEQ + 8;
-  __shared__ __attribute__((aligned(16))) T plds[4][16 * PST_MAX];
+  constexpr int NT_MAX = ATT_MAX_SEQ / 16, NC = ATT_MAX_SEQ / CH, PTS = 40;
+  // P goes through LDS 32 keys at a time (a 16 x 32 tile per wave), so the workgroup's
+  // LDS is ~23 KB and occupancy is set by registers rather than by whole P rows
+  __shared__ __attribute__((aligned(16))) T plds[4][16 * PTS];
   __shared__ __attribute__((aligned(16))) T kv[CH * KST > AD * VST ? CH * KST : AD * VST];
   const T* Q = (const T*)Qp;
   const T* K = (const T*)Kp;
@@ -191,7 +193,6 @@ attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, con
   const int q0 = blockIdx.x * 64 + wave * 16;
   const bool active = q0 < seq;
   const int NT = seq / 16;
-  const int PST = seq + 8;
   const int q = q0 + r;
   const bool qok = q < seq;
 
@@ -265,16 +266,7 @@ attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, con
   sum += __shfl_xor(sum, 16);
   sum += __shfl_xor(sum, 32);
   const float inv = 1.f / sum;
-  T* prow = plds[wave];
-#pragma unroll
-  for (int kt = 0; kt < NT_MAX; ++kt)
-    if (kt < NT) {
-      const t4 pv = {(T)(sv[kt][0] * inv), (T)(sv[kt][1] * inv), (T)(sv[kt][2] * inv), (T)(sv[kt][3] * inv)};
-      *reinterpret_cast<t4*>(prow + r * PST + kt * 16 + 4 * g) = pv;
-    }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  T* ptile = plds[wave];
 
   // 3. O = P V, one 128-key chunk of V^T at a time: 64 rows x 16 chunks of 16 bytes, 4 per thread
   f32x4 oacc[4];
@@ -297,8 +289,20 @@ attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, con
 #pragma unroll
         for (int u = 0; u < CH / 32; ++u) {
           const int kk = c * (CH / 32) + u;
-          if (2 * kk < NT) {
-            const i32x4 pf = *reinterpret_cast<const i32x4*>(prow + r * PST + kk * 32 + g * 8);
+          if (2 * kk < NT) {  // seq % 32 == 0, so tile 2kk+1 is live too
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float* e = sv[2 * kk + h];
+              const t4 pv = {(T)(e[0] * inv), (T)(e[1] * inv), (T)(e[2] * inv), (T)(e[3] * inv)};
+              *reinterpret_cast<t4*>(ptile + r * PTS + h * 16 + 4 * g) = pv;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const i32x4 pf = *reinterpret_cast<const i32x4*>(ptile + r * PTS + g * 8);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
               const i32x4 vf = *reinterpret_cast<const i32x4*>(kv + (dt * 16 + r) * VST + u * 32 + g * 8);
