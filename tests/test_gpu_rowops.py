@@ -205,11 +205,13 @@ def test_qkv_split_and_merge_heads(gpu, dtype, b, s, heads, with_bias):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("b,s,heads,masked", [(2, 128, 12, True), (1, 32, 3, True), (3, 96, 2, False),
-                                               (1, 512, 2, True), (2, 288, 1, True)])
+                                               (1, 512, 2, True), (2, 288, 1, True), (2, 192, 4, True),
+                                               (1, 160, 3, False)])
 def test_attention_fwd(gpu, dtype, b, s, heads, masked):
     """icpp_attention_fwd against fp32 attention on the CPU: the BERT layer's causal mask
-    (-10000 above the diagonal), sequence lengths in each of the kernel's three register
-    buckets (<= 128, <= 256, <= 512), a partial last 64-query block (96, 288) and no mask.
+    (-10000 above the diagonal), sequence lengths for both kernels (direct up to 128 keys,
+    staged from 160 to 512, including 160 and 192 where one 128-key chunk is partial),
+    a partial last 64-query block (96, 160, 288) and no mask.
     Tolerance 1e-2 + 1e-2 |ref| (P is rounded to the data type before P V)."""
     g = torch.Generator().manual_seed(b * 7 + s + heads)
     q = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
