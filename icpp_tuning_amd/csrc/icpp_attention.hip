@@ -209,19 +209,34 @@ attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, con
 #pragma unroll
     for (int j = 0; j < 4; ++j) sv[kt][j] = -INFINITY;
   // 1. scores, one 128-key chunk of K at a time: 128 rows x 8 chunks of 16 bytes, 4 per thread
+  // chunk c+1 is loaded into registers while chunk c multiplies
+  i32x4 pre[4];
+  auto load_k = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = tid + 256 * i, key = c * CH + (x >> 3);
+      if (key < seq) pre[i] = *reinterpret_cast<const i32x4*>(K + ((size_t)bh * seq + key) * AD + (x & 7) * 8);
+    }
+  };
+  auto load_v = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = tid + 256 * i, key = c * CH + (x & 15) * 8;
+      if (key < seq) pre[i] = *reinterpret_cast<const i32x4*>(VT + ((size_t)bh * AD + (x >> 4)) * seq + key);
+    }
+  };
+  load_k(0);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     if (c * CH < seq) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int x = tid + 256 * i;
-        const int kr = x >> 3, kc = x & 7;
-        const int key = c * CH + kr;
-        if (key < seq)
-          *reinterpret_cast<i32x4*>(kv + kr * KST + kc * 8) =
-              *reinterpret_cast<const i32x4*>(K + ((size_t)bh * seq + key) * AD + kc * 8);
+        if (c * CH + (x >> 3) < seq) *reinterpret_cast<i32x4*>(kv + (x >> 3) * KST + (x & 7) * 8) = pre[i];
       }
       __syncthreads();
+      if ((c + 1) * CH < seq) load_k(c + 1);
+      else load_v(0);
       if (active) {
 #pragma unroll
         for (int t = 0; t < CH / 16; ++t) {
@@ -279,13 +294,10 @@ attention_fwd_staged_kernel(const void* Qp, const void* Kp, const void* VTp, con
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int x = tid + 256 * i;
-        const int d = x >> 4, kc = x & 15;
-        const int key = c * CH + kc * 8;
-        if (key < seq)
-          *reinterpret_cast<i32x4*>(kv + d * VST + kc * 8) =
-              *reinterpret_cast<const i32x4*>(VT + ((size_t)bh * AD + d) * seq + key);
+        if (c * CH + (x & 15) * 8 < seq) *reinterpret_cast<i32x4*>(kv + (x >> 4) * VST + (x & 15) * 8) = pre[i];
       }
       __syncthreads();
+      if ((c + 1) * CH < seq) load_v(c + 1);
       if (active) {
 #pragma unroll
         for (int u = 0; u < CH / 32; ++u) {
