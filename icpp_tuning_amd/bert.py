@@ -73,8 +73,8 @@ class BertLayerWeights:
 
 # Longest sequence sent to the fused attention kernel (its limit).  Measured against the
 # batched-product path (split, bmm, scaled masked softmax, bmm, merge), b x s = 32x128 /
-# 16x256 / 8x384 / 8x512: 30.4 / 46.1 / 63.9 / 84.9 us fused against 59.5 / 59.8 / 83.2 /
-# 87.9 us.
+# 16x256 / 8x384 / 8x512: 28.3 / 37.0 / 43.6 / 51.7 us fused against 59.6 / 60.1 / 82.4 /
+# 86.2 us.
 ATTENTION_FUSED_MAX_SEQ = 512
 
 
