@@ -4,17 +4,24 @@
 Headline (BASELINE.json metric, config 2): fused GEMM + bias + GELU(tanh),
 M = N = K = 4096, bf16 in / bf16 out, fp32 accumulate, seeded synthetic
 inputs resident in HBM.  A "step" is one launch of the fused op; ``value`` is
-2*M*N*K*steps / (timed wall time) in TFLOP/s.
+2*M*N*K*steps / (timed wall time) in TFLOP/s.  The steps rotate over enough
+input copies (A, B, bias, C) to exceed the 256 MiB MALL, as every per-op row does,
+so no launch finds its operands cache-resident from the previous one.
 
-The same JSON line also carries
-  roofline      the kernel's average duration from HIP events on its stream,
-                against the dense bf16 MFMA peak (2516.6 TFLOP/s)
-  cpu_baseline  the CPU oracle (fp32 eager torch, oracle/ops.py) on a bounded
-                row-slice of the same problem, on this host's cores
-  ops           TFLOP/s and % of peak (or GB/s and % of 8 TB/s for HBM-bound
-                shapes) for every benchmark configuration, with the tuner's
-                time-to-best (prune + rank, compile = 0 for AOT instances,
-                top-k device benchmark)
+Output (stdout):
+  one earlier line  {"ops": [...]}: the full per-op table (tuned config, TFLOP/s,
+                    % of MFMA peak or of HBM bandwidth, tuner time-to-best split)
+  the last line     the compact headline record the driver parses:
+    roofline        the kernel's average duration from HIP events on its stream,
+                    against the dense bf16 MFMA peak (2516.6 TFLOP/s, quoted at the
+                    2.4 GHz maximum shader clock), plus the shader clock sustained
+                    under this load (live, icpp_clock_probe) and the fraction of
+                    the peak at that clock
+    cpu_baseline    the CPU oracle (fp32 eager torch, oracle/ops.py) on a bounded
+                    sample of the headline problem, on this host's cores, with a
+                    per-op entry for all five benchmark configurations
+    ops             one short entry per per-op row
+Per-op progress lines go to stderr.
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--quick] [--no-ops]
 """
@@ -36,6 +43,9 @@ METRIC = "TFLOP/s and % MFMA peak per fused op on 1 MI355X; tuner time-to-best"
 PEAK_BF16 = 2516.6
 PEAK_FP8 = 5033.2
 HBM_GBPS = 8000.0
+PEAK_SCLK_MHZ = 2400.0   # the shader clock the datasheet peaks are quoted at
+CACHE_BYTES = 600 << 20  # input copies rotate over more than the 256 MiB MALL + L2
+FINAL_LINE_MAX = 8000    # bytes: the driver reads the tail of stdout
 
 
 def _events():
@@ -44,26 +54,84 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_steps(fn, steps: int, warmup: int):
-    """Warm up, then time exactly `steps` calls bracketed by synchronize."""
+def time_steps(steps_fns, steps: int, warmup: int):
+    """Warm up, then time exactly `steps` calls (round-robin over the callables)
+    bracketed by synchronize; returns (wall seconds, event seconds)."""
     import torch
 
-    for _ in range(warmup):
-        fn()
+    fns = list(steps_fns)
+    for i in range(warmup):
+        fns[i % len(fns)]()
     torch.cuda.synchronize()
     s, e = _events()
     t0 = time.perf_counter()
     s.record()
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fns[i % len(fns)]()
     e.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return wall, s.elapsed_time(e) / 1e3
 
 
-def cpu_baseline(target_seconds: float = 12.0):
-    """Oracle GEMM+bias+GELU on CPU over a row slice of config 2, median of 3."""
+def sustained_clock(steps_fns, kernel_s: float, seconds: float = 0.25):
+    """Shader clock held while the step kernel runs back to back: the clock probe
+    (one sleeping wave, on a side stream) spans most of a ~`seconds` burst of steps
+    on the current stream.  Returns (MHz, probe window in s, average kernel seconds
+    over the burst, from HIP events on the current stream)."""
+    import torch
+
+    from icpp_tuning_amd._lib import lib
+
+    fns = list(steps_fns)
+    n = max(20, int(seconds / max(kernel_s, 1e-6)))
+    window = 0.8 * n * kernel_s
+    out = torch.zeros(2, dtype=torch.int64, device="cuda")
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    s, e = _events()
+    s.record()
+    for i in range(n // 10):  # the probe starts once the chip is loaded
+        fns[i % len(fns)]()
+    with torch.cuda.stream(side):
+        lib().call("icpp_clock_probe", out.data_ptr(), float(window), side.cuda_stream)
+    for i in range(n // 10, n):
+        fns[i % len(fns)]()
+    e.record()
+    torch.cuda.synchronize()
+    ticks, rt = (int(v) for v in out.cpu())
+    return (ticks / rt * 100.0 if rt > 0 else None), rt / 1e8, s.elapsed_time(e) / 1e3 / n
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _median_run(fn, reps: int = 3) -> float:
+    fn()  # warmup
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_baselines(per_op_s: float = 4.0):
+    """The reference's torch programs, restated in fp32 eager on the CPU (oracle/ops.py),
+    timed on this host's cores: config 2 (the headline) plus one shape of every other
+    benchmark configuration.  Each sample is sized from a short probe so that warmup
+    + 3 reps take about ``per_op_s``; FLOPs are the GPU rows' numerator (2 M N K, or
+    2 N OH OW F C KH KW for conv; epilogue / LayerNorm work not counted)."""
     import torch
 
     from icpp_tuning_amd import inputs as I
@@ -71,26 +139,51 @@ def cpu_baseline(target_seconds: float = 12.0):
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    K = N = 4096
-    probe_rows = 256
-    d = I.config2(4096, N, K)
-    A, B, bias = d["A"], d["B"], d["bias"]
-    t0 = time.perf_counter()
-    O.gemm_bias_act_ref(A[:probe_rows], B, bias, "gelu_tanh")
-    per_row = (time.perf_counter() - t0) / probe_rows
-    rows = int(max(probe_rows, min(4096, target_seconds / 3.0 / max(per_row, 1e-9))))
-    rows = max(probe_rows, rows // 64 * 64)
-    O.gemm_bias_act_ref(A[:rows], B, bias, "gelu_tanh")  # warmup
-    ts = []
-    for _ in range(3):
+    per = {}
+
+    def sized(name, full_units, unit_flops, run, what):
+        # probe on a few units, then scale so one run takes ~per_op_s / 4
+        probe = max(1, min(full_units, full_units // 16))
         t0 = time.perf_counter()
-        O.gemm_bias_act_ref(A[:rows], B, bias, "gelu_tanh")
-        ts.append(time.perf_counter() - t0)
-    ts.sort()
-    tflops = 2.0 * rows * N * K / ts[1] / 1e12
-    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle gemm_bias_act_ref(gelu_tanh) fp32 eager on CPU, rows 0..{rows} of the 4096^3 "
-                      f"bf16 config-2 inputs (M={rows}, N=K=4096), median of 3 after 1 warmup"}
+        run(probe)
+        per_unit = (time.perf_counter() - t0) / probe
+        units = int(max(probe, min(full_units, per_op_s / 4.0 / max(per_unit, 1e-9))))
+        t = _median_run(lambda: run(units))
+        per[name] = {"tflops": round(unit_flops * units / t / 1e12, 4), "seconds": round(t, 4),
+                     "sample": what.format(units=units)}
+
+    # config 1: GEMM 1024^3 (gemm.py:19-21), rows of A
+    d1 = I.config1()
+    sized("gemm_1024_f16", 1024, 2.0 * 1024 * 1024, lambda r: O.gemm_ref(d1["A"][:r], d1["B"]),
+          "gemm_ref, rows 0..{units} of the 1024^3 fp16 inputs")
+    # config 2: GEMM+bias+GELU-tanh 4096^3 (gemm_bias_act.py:43-47 + end2end.py:37-38), rows of A
+    d2 = I.config2()
+    sized("gemm_bias_gelu_tanh_4096_bf16", 4096, 2.0 * 4096 * 4096,
+          lambda r: O.gemm_bias_act_ref(d2["A"][:r], d2["B"], d2["bias"], "gelu_tanh"),
+          "gemm_bias_act_ref(gelu_tanh), rows 0..{units} of the 4096^3 bf16 inputs")
+    del d2
+    # config 3: GEMM+bias+LN at N=1024 (gemm_bias_layernorm.py:43-49), rows of A
+    d3 = I.config3(8192, 1024, 4096)
+    sized("gemm_bias_layernorm_8192x1024x4096_f16", 8192, 2.0 * 1024 * 4096,
+          lambda r: O.gemm_bias_layernorm_ref(d3["A"][:r], d3["B"], d3["bias"], d3["gamma"], d3["beta"]),
+          "gemm_bias_layernorm_ref, rows 0..{units} of M=8192, N=1024, K=4096 fp16")
+    del d3
+    # config 4: conv 56x56x64 -> 64 (conv2d.py:35-62), images of the batch
+    d4 = I.config4(32, 56, 56, 64, 64)
+    sized("conv2d_b32_56x56x64_f16", 32, 2.0 * 56 * 56 * 64 * 64 * 9,
+          lambda b: O.conv2d_nhwc_ref(d4["X"][:b], d4["W"]),
+          "conv2d_nhwc_ref, images 0..{units} of batch 32, 56x56x64 -> 64, 3x3 s1 p1")
+    del d4
+    # config 5: fp8 GEMM+bias+SiLU at M=256, N=K=4096 (dequantised fp32), rows of A
+    d5 = I.config5(256, 4096, 4096)
+    sized("fp8_gemm_bias_silu_256x4096x4096", 256, 2.0 * 4096 * 4096,
+          lambda r: O.fp8_gemm_bias_act_ref(d5["A"][:r], d5["B"], d5["scale_a"], d5["scale_b"], d5["bias"], "silu"),
+          "fp8_gemm_bias_act_ref(silu) on dequantised e4m3 inputs, rows 0..{units} of M=256, N=K=4096")
+    head = per["gemm_bias_gelu_tanh_4096_bf16"]
+    return {"value": head["tflops"], "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": "oracle " + head["sample"] + ", fp32 eager torch on CPU, median of 3 after 1 warmup",
+            "per_op": per}
 
 
 def _load_traffic(workload: str):
@@ -289,6 +382,131 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
     return rows
 
 
+def _shape_str(shape) -> str:
+    if isinstance(shape, dict):
+        if "OC" in shape:
+            return f"b{shape['N']} {shape['H']}x{shape['W']}x{shape['C']}->{shape['OC']}"
+        if "batch" in shape:
+            return f"b{shape['batch']} s{shape['seq']}"
+        return "x".join(str(shape[k]) for k in ("M", "N", "K") if k in shape)
+    return str(shape)
+
+
+def compact_ops(rows):
+    """One short entry per per-op row for the final line (the full rows go on an
+    earlier stdout line)."""
+    out = []
+    for r in rows:
+        e = {"op": r["op"], "shape": _shape_str(r.get("shape")), "us": round(r["ms"] * 1e3, 2)}
+        if "tflops" in r and r.get("bound") != "hbm" and "pct_mfma_peak" in r:
+            e["pct_peak"] = r["pct_mfma_peak"]
+        if r.get("bound") == "hbm":
+            e["pct_hbm"] = r["pct_hbm"]
+        if "config" in r:
+            e["cfg"] = r["config"]
+        if "speedup" in r:
+            e["x_torch"] = r["speedup"]
+        out.append(e)
+    return out
+
+
+def final_line(head: dict, rows=None, cpu=None) -> str:
+    """The compact last stdout line: headline fields, roofline, cpu_baseline (per-op
+    TFLOP/s), the tuner split and one short entry per per-op row."""
+    out = dict(head)
+    if cpu is not None:
+        out["cpu_baseline"] = {k: v for k, v in cpu.items() if k != "per_op"}
+        out["cpu_baseline"]["per_op_tflops"] = {k: v["tflops"] for k, v in cpu.get("per_op", {}).items()}
+    if rows:
+        out["ops"] = compact_ops(rows)
+    line = json.dumps(out, separators=(",", ":"))
+    if len(line) > FINAL_LINE_MAX and rows:  # keep the headline parseable: drop the per-op configs first
+        for e in out["ops"]:
+            e.pop("cfg", None)
+        line = json.dumps(out, separators=(",", ":"))
+    if len(line) > FINAL_LINE_MAX:
+        out.pop("ops", None)
+        line = json.dumps(out, separators=(",", ":"))
+    return line
+
+
+def headline(args):
+    """Tune, then time the config-2 kernel over rotated input copies; returns the
+    headline record (metric, value, roofline with the sustained clock, tuner split)."""
+    import torch
+
+    from icpp_tuning_amd import inputs as I
+    from icpp_tuning_amd.autotuner.interface import select_best, tune
+    from icpp_tuning_amd.kernels import gemm_bias_act as GBA
+
+    M = N = K = 4096
+    desc = GBA.descriptor("gelu_tanh", "bf16")
+    t_sel = time.perf_counter()
+    cfg, score = select_best(desc, M=M, N=N, K=K)
+    select_s = time.perf_counter() - t_sel
+    tuned = None
+    if args.instance:
+        from icpp_tuning_amd.kernels._base import family_instances, raw_from_inst
+
+        match = [i for i in family_instances("gemm") if i.name == args.instance]
+        if not match:
+            raise SystemExit(f"bench.py: unknown instance {args.instance}")
+        cfg = raw_from_inst(match[0])
+    else:
+        # 30 launches per timed batch (~3.5 ms): shorter bursts run at a boost clock the
+        # steady state does not keep, and flip the choice between near-equal tiles
+        tuned = tune(desc, top_k=4, warmup=5, reps=30, input_copies="auto", M=M, N=N, K=K)
+        cfg = tuned.best_config
+    kern = GBA.build_kernel(M, N, K, config=cfg, act="gelu_tanh", dtype="bf16")
+    set_bytes = 2 * (M * K + K * N + M * N + N)
+    copies = max(1, -(-CACHE_BYTES // set_bytes))
+    sets = []
+    for c in range(copies):
+        d = I.config2(M, N, K, device="cuda") if c == 0 else {k: v.clone() for k, v in sets[0].items() if k != "C"}
+        d["C"] = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        sets.append(d)
+    steps = [(lambda d=d: kern(d["A"], d["B"], d["bias"], out=d["C"])) for d in sets]
+    wall, ev = time_steps(steps, args.steps, args.warmup)
+    flops = 2.0 * M * N * K
+    value = flops * args.steps / wall / 1e12
+    kernel_s = ev / args.steps
+    achieved = flops / kernel_s / 1e12
+    sclk, window, burst_kernel_s = sustained_clock(steps, kernel_s)
+    workload = "gemm_bias_gelu_tanh_4096x4096x4096_bf16"
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16, 4), "traffic": _load_traffic(workload),
+            "kernel_us": round(kernel_s * 1e6, 2), "peak_sclk_mhz": PEAK_SCLK_MHZ}
+    if sclk:
+        # the clock is measured over a ~0.25 s burst (the steady state), so the
+        # clock-scaled fraction uses the kernel time of that same burst
+        roof["sclk_mhz"] = round(sclk, 1)
+        roof["sclk_window_s"] = round(window, 3)
+        roof["kernel_us_at_sclk"] = round(burst_kernel_s * 1e6, 2)
+        roof["peak_at_sclk"] = round(PEAK_BF16 * sclk / PEAK_SCLK_MHZ, 1)
+        roof["frac_at_sclk"] = round(flops / burst_kernel_s / 1e12 / (PEAK_BF16 * sclk / PEAK_SCLK_MHZ), 4)
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) / N(0,1/sqrt(K)))",
+        "config": {"workload": workload, "M": M, "N": N, "K": K, "op": "gemm+bias+gelu_tanh",
+                   "tile": desc.format_config(cfg), "input_copies": copies, "parallelism": "single-gpu"},
+        "roofline": roof,
+    }
+    if tuned is not None:
+        out["tuner"] = {"time_to_best_s": round(tuned.time_to_best_s, 3), "prune_rank_s": round(tuned.prune_rank_s, 4),
+                        "compile_s": round(tuned.compile_s, 4), "bench_s": round(tuned.bench_s, 3),
+                        "formula_top1": desc.format_config(tuned.formula_top1),
+                        "formula_top1_ms": round(tuned.formula_top1_ms, 5), "select_best_s": round(select_s, 4),
+                        "candidates": len(tuned.candidates)}
+    print(f"[bench] headline {workload} {roof['kernel_us']} us/launch, {achieved:.1f} TFLOP/s "
+          f"({100 * roof['frac']:.1f}% of peak), sclk {sclk and round(sclk)} MHz, "
+          f"{copies} input copies", file=sys.stderr, flush=True)
+    del sets, steps
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -308,9 +526,16 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
     args = ap.parse_args()
-    if args.calibrate_copy:
-        import torch
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
+              "(DESIGN.md describes how the path would shard).", file=sys.stderr)
+        return 2
+    import torch
 
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    if args.calibrate_copy:
         src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -319,76 +544,18 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes_read": src.numel() * 4, "calibrate_copy_bytes_written": dst.numel() * 4}))
         return 0
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
-              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
-        return 2
-
-    import torch
-
-    from icpp_tuning_amd import inputs as I
-    from icpp_tuning_amd.autotuner.interface import select_best
-    from icpp_tuning_amd.kernels import gemm_bias_act as GBA
-
-    if not torch.cuda.is_available():
-        print("bench.py: no GPU visible", file=sys.stderr)
-        return 1
     if args.op:  # one family of per-op rows only (profiling runs)
         print(json.dumps({"ops": bench_ops(args.quick, args.op, args.op_configs)}), flush=True)
         return 0
-    M = N = K = 4096
-    desc = GBA.descriptor("gelu_tanh", "bf16")
-    t_sel = time.perf_counter()
-    cfg, score = select_best(desc, M=M, N=N, K=K)
-    select_s = time.perf_counter() - t_sel
-    # the tuned choice for this shape (measured top-k); fall back to the formula top-1
-    from icpp_tuning_amd.autotuner.interface import tune
-
-    if args.instance:
-        from icpp_tuning_amd.kernels._base import family_instances, raw_from_inst
-
-        match = [i for i in family_instances("gemm") if i.name == args.instance]
-        if not match:
-            print(f"bench.py: unknown instance {args.instance}", file=sys.stderr)
-            return 2
-        cfg, tuned = raw_from_inst(match[0]), None
-    else:
-        # 30 launches per timed batch (~3.5 ms): shorter bursts run at a boost clock the
-        # steady state does not keep, and flip the choice between near-equal tiles
-        res = tune(desc, top_k=4, warmup=5, reps=30, M=M, N=N, K=K)
-        cfg, tuned = res.best_config, res
-    kern = GBA.build_kernel(M, N, K, config=cfg, act="gelu_tanh", dtype="bf16")
-    d = I.config2(M, N, K, device="cuda")
-    A, B, bias = d["A"], d["B"], d["bias"]
-    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    step = lambda: kern(A, B, bias, out=C)  # noqa: E731
-    wall, ev = time_steps(step, args.steps, args.warmup)
-    flops = 2.0 * M * N * K
-    value = flops * args.steps / wall / 1e12
-    achieved = flops / (ev / args.steps) / 1e12
-    workload = "gemm_bias_gelu_tanh_4096x4096x4096_bf16"
-    out = {
-        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) / N(0,1/sqrt(K)))",
-        "config": {"workload": workload, "M": M, "N": N, "K": K, "op": "gemm+bias+gelu_tanh",
-                   "tile": desc.format_config(cfg), "parallelism": "single-gpu"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16, 4), "traffic": _load_traffic(workload),
-                     "kernel_us": round(ev / args.steps * 1e6, 2)},
-    }
-    if tuned is not None:  # noqa: SIM102
-        out["tuner"] = {"time_to_best_s": round(tuned.time_to_best_s, 3), "prune_rank_s": round(tuned.prune_rank_s, 4),
-                        "compile_s": round(tuned.compile_s, 4), "bench_s": round(tuned.bench_s, 3),
-                        "formula_top1": desc.format_config(tuned.formula_top1),
-                        "formula_top1_ms": round(tuned.formula_top1_ms, 5), "select_best_s": round(select_s, 4)}
-    del A, B, bias, C, d
-    torch.cuda.empty_cache()
+    head = headline(args)
+    rows = None
     if not args.no_ops and not args.headline_only_kernel:
-        out["ops"] = bench_ops(args.quick)
+        rows = bench_ops(args.quick)
+        print(json.dumps({"ops": rows}), flush=True)
+    cpu = None
     if not args.no_cpu and not args.headline_only_kernel:
-        out["cpu_baseline"] = cpu_baseline()
-    print(json.dumps(out), flush=True)
+        cpu = cpu_baselines()
+    print(final_line(head, rows, cpu), flush=True)
     return 0
 
 

@@ -235,6 +235,17 @@ int icpp_merge_heads(int dtype, const void* X, void* Y, int batch, int seq, int 
 int icpp_attention_fwd(int dtype, const void* Q, const void* K, const void* VT, const void* mask, float scale, void* O,
                        int batch, int seq, int heads, int head_dim, void* stream);
 
+/*
+ * Measurement aid, no counterpart in the reference (whose harness reads clocks
+ * from the NVIDIA profiler, motivation/exp_2/profile.py:39-53): one wave reads the
+ * shader-clock counter and the 100 MHz real-time counter, sleeps until `seconds`
+ * of real time have passed, and writes out[0] = shader-clock ticks, out[1] =
+ * real-time ticks (device memory, 2 x uint64, 8-byte aligned).  Launched on its own
+ * stream beside a kernel, out[0] / out[1] * 100 MHz is the shader clock the chip
+ * held under that load.  seconds in (0, 10].
+ */
+int icpp_clock_probe(unsigned long long* out, double seconds, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
