@@ -236,6 +236,22 @@ int icpp_attention_fwd(int dtype, const void* Q, const void* K, const void* VT, 
                        int batch, int seq, int heads, int head_dim, void* stream);
 
 /*
+ * icpp_gemm without a workspace argument and without any device allocation: no
+ * counterpart in the reference.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as icpp_gemm; with
+ * split_k > 1 the fp32 partials live in a static device array of
+ * ICPP_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), so calls need
+ * split_k * M * N * 4 <= ICPP_NOALLOC_SCRATCH_BYTES (ICPP_E_WORKSPACE otherwise).
+ * Every call on one GPU shares that array: calls that overlap in time on one GPU
+ * race; calls serialised on one stream are safe.
+ */
+#define ICPP_NOALLOC_SCRATCH_BYTES (16u << 20)
+int icpp_gemm_noalloc(int inst, const void* A, const void* B, const void* bias, void* C,
+                      int M, int N, int K, int lda, int ldb, int ldc, int act,
+                      float scale_a, float scale_b, int split_k, void* stream);
+
+/*
  * Measurement aid, no counterpart in the reference (whose harness reads clocks
  * from the NVIDIA profiler, motivation/exp_2/profile.py:39-53): one wave reads the
  * shader-clock counter and the 100 MHz real-time counter, sleeps until `seconds`
