@@ -8,8 +8,12 @@ Restates the reference's end-to-end harness layer (evaluation/end2end.py
   FFN out            LN(inter @ Wo2 + bo2 + x)       icpp_gemm_bias_residual_layernorm  (:84-87)
 
 The attention core (:52-71: scores = q k^T / sqrt(d) + causal mask, softmax,
-attention @ v) runs as in the reference -- two batched library GEMMs -- with
-the row softmax of this library; dropout is p = 0 there (:230).  Like the
+attention @ v; dropout is p = 0 there, :230) dispatches by shape: head size 64
+and a sequence that is a multiple of 32 up to 512 go through the head split
+(icpp_qkv_split_heads) and one fused launch (icpp_attention_fwd: per-wave K
+streaming up to 128 keys, K / V^T staged through LDS from 160 keys); any other
+shape runs the scores and P V as batched library products around this library's
+scaled masked softmax.  Like the
 reference, the layer takes the QKV projections as given activations
 (``qkv_kernel[layer] + qkv_bias[layer]``, :47) rather than computing them.
 

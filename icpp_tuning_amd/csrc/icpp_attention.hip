@@ -10,8 +10,8 @@
 // Per wave:
 //   1. S = Q K^T for all keys with 16x16x32 MFMAs: the 16 x 64 query block stays
 //      in two fragments, every 16-key tile of K [seq, 64] is read straight from
-//      global memory (16 contiguous bytes per lane).  S stays in registers (up to
-//      512 keys), scaled and masked in fp32.
+//      global memory (16 contiguous bytes per lane).  S stays in registers (this
+//      direct kernel serves up to 128 keys), scaled and masked in fp32.
 //   2. Row softmax over the registers: each query row is spread over the 4 lanes
 //      r, r+16, r+32, r+48, so the max and the sum take two cross-lane steps.
 //   3. P is rounded to the data type and written to the wave's LDS rows (stride

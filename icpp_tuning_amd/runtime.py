@@ -23,11 +23,16 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def _check(t: Optional[torch.Tensor], name: str, dtype: Optional[torch.dtype] = None, shape=None) -> int:
+def _check(t: Optional[torch.Tensor], name: str, dtype: Optional[torch.dtype] = None, shape=None,
+           device: Optional[torch.device] = None) -> int:
+    """Device pointer of t after checking that it lives on the GPU (on `device` when
+    given), is contiguous and has the dtype / shape asked for; None for None."""
     if t is None:
         return None
     if not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor (got {t.device})")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, the other operands on {device}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
     if dtype is not None and t.dtype != dtype:
@@ -57,11 +62,11 @@ def gemm(inst: int, dtype: str, a: torch.Tensor, b: torch.Tensor, bias: Optional
         raise ValueError(f"inner dimensions differ: a is {tuple(a.shape)}, b is {tuple(b.shape)}")
     tdt = TORCH_DTYPE[dtype]
     pa = _check(a, "a", tdt)
-    pb = _check(b, "b", tdt)
-    pbias = _check(bias, "bias", BIAS_DTYPE[dtype], (N,))
+    pb = _check(b, "b", tdt, device=a.device)
+    pbias = _check(bias, "bias", BIAS_DTYPE[dtype], (N,), device=a.device)
     if out is None:
         out = torch.empty((M, N), dtype=OUT_DTYPE[dtype], device=a.device)
-    pc = _check(out, "out", OUT_DTYPE[dtype], (M, N))
+    pc = _check(out, "out", OUT_DTYPE[dtype], (M, N), device=a.device)
     need = workspace_bytes("gemm", inst, M, N, K, split_k)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = alloc_workspace(need, a.device)
@@ -81,12 +86,12 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
     M, K = a.shape
     _, N = b.shape
     h = torch.float16
-    pa, pb = _check(a, "a", h), _check(b, "b", h, (K, N))
-    pbias = _check(bias, "bias", h, (N,))
-    pg, pbe = _check(gamma, "gamma", h, (N,)), _check(beta, "beta", h, (N,))
+    pa, pb = _check(a, "a", h), _check(b, "b", h, (K, N), device=a.device)
+    pbias = _check(bias, "bias", h, (N,), device=a.device)
+    pg, pbe = _check(gamma, "gamma", h, (N,), device=a.device), _check(beta, "beta", h, (N,), device=a.device)
     if out is None:
         out = torch.empty((M, N), dtype=h, device=a.device)
-    py = _check(out, "out", h, (M, N))
+    py = _check(out, "out", h, (M, N), device=a.device)
     need = workspace_bytes(family, inst, M, N, K, 1)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = alloc_workspace(need, a.device)
@@ -96,7 +101,7 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
         lib().call("icpp_gemm_bias_layernorm", FAMILY[family], inst, pa, pb, pbias, pg, pbe, py,
                    M, N, K, float(eps), pws, wsb, _stream())
     else:
-        pr = _check(residual, "residual", h, (M, N))
+        pr = _check(residual, "residual", h, (M, N), device=a.device)
         lib().call("icpp_gemm_bias_residual_layernorm", FAMILY[family], inst, pa, pb, pbias, pr, pg, pbe, py,
                    M, N, K, float(eps), pws, wsb, _stream())
     return out
@@ -116,8 +121,8 @@ def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, st
     OH = (H + 2 * pad - dilation * (KH - 1) - 1) // stride + 1
     OW = (W + 2 * pad - dilation * (KW - 1) - 1) // stride + 1
     h = torch.float16
-    px, pw = _check(x, "x", h), _check(w, "w", h)
-    py = _check(y, "y", h, (N, OH, OW, F))
+    px, pw = _check(x, "x", h), _check(w, "w", h, device=x.device)
+    py = _check(y, "y", h, (N, OH, OW, F), device=x.device)
     Mg, Kg = N * OH * OW, KH * KW * C
     need = workspace_bytes("conv2d", inst, Mg, F, Kg, split_k)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
@@ -133,11 +138,11 @@ def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, st
     if bn is not None:
         if len(bn) != 4:
             raise ValueError("bn must be (gamma, beta, mean, var)")
-        pbn = [_check(t, nm, h, (F,)) for t, nm in zip(bn, ("gamma", "beta", "mean", "var"))]
+        pbn = [_check(t, nm, h, (F,), device=x.device) for t, nm in zip(bn, ("gamma", "beta", "mean", "var"))]
         flags |= CONV_EPI["bn"] | (CONV_EPI["var_clamp"] if var_clamp else 0)
     elif var_clamp:
         raise ValueError("var_clamp needs bn")
-    pres = _check(residual, "residual", h, (N, OH, OW, F))
+    pres = _check(residual, "residual", h, (N, OH, OW, F), device=x.device)
     if residual is not None:
         flags |= CONV_EPI["residual"]
     lib().call("icpp_conv2d_nhwc_fused", inst, px, pw, py, pres, *pbn, float(eps), flags, ACT[act],
@@ -167,11 +172,12 @@ def layernorm_fwd(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps
     x2 = _rows(x, "x")
     M, N = x2.shape
     dt = ROW_DTYPE[x.dtype]
-    pw, pb = _check(weight, "weight", x.dtype, (N,)), _check(bias, "bias", x.dtype, (N,))
+    pw = _check(weight, "weight", x.dtype, (N,), device=x.device)
+    pb = _check(bias, "bias", x.dtype, (N,), device=x.device)
     if out is None:
         out = torch.empty_like(x)
     y2 = _rows(out, "out")
-    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype:
+    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype or out.device != x.device:
         raise ValueError("out must match x")
     mean = torch.empty((M,), dtype=torch.float32, device=x.device)
     rstd = torch.empty((M,), dtype=torch.float32, device=x.device)
@@ -186,12 +192,12 @@ def layernorm_bwd(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, mean:
     x2 = _rows(x.contiguous(), "x")
     dy2 = _rows(dy.contiguous(), "dy")
     M, N = x2.shape
-    if tuple(dy2.shape) != (M, N) or dy.dtype != x.dtype:
+    if tuple(dy2.shape) != (M, N) or dy.dtype != x.dtype or dy.device != x.device:
         raise ValueError("dy must match x")
     dt = ROW_DTYPE[x.dtype]
-    pw = _check(weight, "weight", x.dtype, (N,))
-    pm = _check(mean, "mean", torch.float32, (M,))
-    pr = _check(rstd, "rstd", torch.float32, (M,))
+    pw = _check(weight, "weight", x.dtype, (N,), device=x.device)
+    pm = _check(mean, "mean", torch.float32, (M,), device=x.device)
+    pr = _check(rstd, "rstd", torch.float32, (M,), device=x.device)
     dx = torch.empty((M, N), dtype=x.dtype, device=x.device)
     dw = torch.empty((N,), dtype=weight.dtype, device=x.device)
     db = torch.empty((N,), dtype=weight.dtype, device=x.device)
@@ -209,7 +215,7 @@ def softmax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor
     if out is None:
         out = torch.empty_like(x)
     y2 = _rows(out, "out")
-    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype:
+    if tuple(y2.shape) != (M, N) or out.dtype != x.dtype or out.device != x.device:
         raise ValueError("out must match x")
     lib().call("icpp_softmax", DTYPE[ROW_DTYPE[x.dtype]], x2.data_ptr(), y2.data_ptr(), M, N, x2.stride(0),
                y2.stride(0), _stream())
@@ -227,13 +233,15 @@ def softmax_scaled_masked(x: torch.Tensor, scale: float, mask: Optional[torch.Te
     y2 = _rows(out, "out")
     if tuple(y2.shape) != (M, N) or out.dtype != x.dtype:
         raise ValueError("out must match x")
+    if out.device != x.device:
+        raise ValueError(f"out is on {out.device}, x on {x.device}")
     pm, rows = None, 1
     if mask is not None:
         if mask.dtype != x.dtype or mask.dim() != 2 or mask.shape[1] != N or not mask.is_contiguous():
             raise ValueError(f"mask must be a contiguous [R, {N}] {x.dtype} tensor")
         if M % mask.shape[0]:
             raise ValueError("the number of rows must be a multiple of the mask's")
-        pm, rows = mask.data_ptr(), mask.shape[0]
+        pm, rows = _check(mask, "mask", device=x.device), mask.shape[0]
     lib().call("icpp_softmax_scaled_masked", DTYPE[ROW_DTYPE[x.dtype]], x2.data_ptr(), y2.data_ptr(), pm,
                float(scale), M, N, x2.stride(0), y2.stride(0), rows, _stream())
     return out
@@ -254,12 +262,14 @@ def qkv_split_heads(qkv: torch.Tensor, heads: int, bias: Optional[torch.Tensor] 
         raise ValueError(f"qkv_split_heads: last dim {w} != 3 * heads * {HEAD_DIM}")
     if bias is not None and (bias.dtype != qkv.dtype or not bias.is_contiguous() or bias.numel() != w):
         raise ValueError("qkv_split_heads: bias must be a contiguous [3H] tensor of qkv's dtype")
+    pqkv = _check(qkv, "qkv")
+    pbias = _check(bias, "bias", device=qkv.device)
     q = torch.empty((b * heads, s, HEAD_DIM), dtype=qkv.dtype, device=qkv.device)
     t = torch.empty((b * heads, HEAD_DIM, s), dtype=qkv.dtype, device=qkv.device)
     u = torch.empty_like(q)
     k, v = (t, u) if layout == 0 else (u, t)
-    lib().call("icpp_qkv_split_heads", DTYPE[ROW_DTYPE[qkv.dtype]], qkv.data_ptr(),
-               bias.data_ptr() if bias is not None else None, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+    lib().call("icpp_qkv_split_heads", DTYPE[ROW_DTYPE[qkv.dtype]], pqkv, pbias, q.data_ptr(), k.data_ptr(),
+               v.data_ptr(),
                b, s, heads, HEAD_DIM, int(layout), _stream())
     return q, k, v
 
@@ -275,11 +285,13 @@ def attention_fwd(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, batch: int
         raise ValueError("attention_fwd: q, k [b*h, s, 64] and vt [b*h, 64, s], contiguous, one dtype")
     if mask is not None and (mask.shape != (s, s) or mask.dtype != q.dtype or not mask.is_contiguous()):
         raise ValueError("attention_fwd: mask must be a contiguous [seq, seq] tensor of q's dtype")
+    pq = _check(q, "q")
+    pk, pvt = _check(k, "k", device=q.device), _check(vt, "vt", device=q.device)
+    pmask = _check(mask, "mask", device=q.device)
     heads = bh // batch
     o = torch.empty((batch, s, heads * HEAD_DIM), dtype=q.dtype, device=q.device)
-    lib().call("icpp_attention_fwd", DTYPE[ROW_DTYPE[q.dtype]], q.data_ptr(), k.data_ptr(), vt.data_ptr(),
-               mask.data_ptr() if mask is not None else None, float(scale), o.data_ptr(), batch, s, heads,
-               HEAD_DIM, _stream())
+    lib().call("icpp_attention_fwd", DTYPE[ROW_DTYPE[q.dtype]], pq, pk, pvt, pmask, float(scale), o.data_ptr(),
+               batch, s, heads, HEAD_DIM, _stream())
     return o
 
 
@@ -288,9 +300,10 @@ def merge_heads(ctx: torch.Tensor, batch: int) -> torch.Tensor:
     if ctx.dim() != 3 or ctx.shape[2] != HEAD_DIM or ctx.dtype not in (torch.float16, torch.bfloat16) \
             or not ctx.is_contiguous() or ctx.shape[0] % batch:
         raise ValueError("merge_heads: ctx must be a contiguous [batch*heads, seq, 64] f16 / bf16 tensor")
+    pctx = _check(ctx, "ctx")
     heads, s = ctx.shape[0] // batch, ctx.shape[1]
     y = torch.empty((batch, s, heads * HEAD_DIM), dtype=ctx.dtype, device=ctx.device)
-    lib().call("icpp_merge_heads", DTYPE[ROW_DTYPE[ctx.dtype]], ctx.data_ptr(), y.data_ptr(), batch, s, heads,
+    lib().call("icpp_merge_heads", DTYPE[ROW_DTYPE[ctx.dtype]], pctx, y.data_ptr(), batch, s, heads,
                HEAD_DIM, _stream())
     return y
 

@@ -23,6 +23,16 @@ independent of its own formula):
                                 k -> (kh, kw, c) map of conv2d.py:242-250)
   fp8_gemm_bias_act_ref         exact fp8 e4m3 decode table from the OCP spec
                                 (sign/exponent/mantissa bit arithmetic)
+  conv2d_bn_act_ref             torch batch_norm (eval), fp64 loops, identity /
+                                residual / var-clamp special cases
+  layernorm_fwd_ref / _bwd_ref  F.layer_norm, autograd, constant rows
+  softmax_ref, softmax_scaled_masked_ref
+                                torch.softmax, row-sum / shift invariants
+  qkv_split_heads_ref, merge_heads_ref
+                                explicit index loops over (batch, head, seq, d)
+  attention_ref                 fp64 scaled_dot_product_attention with the additive
+                                causal mask, and fp64 loops per (batch, head)
+  bert_layer_ref                an fp64 SDPA / layer_norm / gelu composition
   reference_configs             evaluation CSV top-1 configs and scores
                                 (tests/golden/formula_scores.json)
 """

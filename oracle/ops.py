@@ -206,15 +206,6 @@ def conv_out_hw(H, W, KH, KW, S, P, D=1):
     return (H + 2 * P - D * (KH - 1) - 1) // S + 1, (W + 2 * P - D * (KW - 1) - 1) // S + 1
 
 
-def quantize_fp8(x: torch.Tensor):
-    """Per-tensor e4m3fn quantisation with scale = amax / 448."""
-    x = x.float()
-    amax = x.abs().max().clamp_min(1e-12)
-    scale = (amax / FP8_MAX).item()
-    q = (x / scale).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
-    return q, scale
-
-
 def fp8_gemm_bias_act_ref(Aq, Bq, scale_a: float, scale_b: float, bias, act: str = "silu") -> torch.Tensor:
     """act(scale_a*scale_b * deq(Aq) @ deq(Bq) + bias) in fp32 (no reference kernel exists;
     this is the dequantised-fp32 oracle BASELINE.json names for config 5)."""

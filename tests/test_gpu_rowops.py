@@ -212,15 +212,20 @@ def test_attention_fwd(gpu, dtype, b, s, heads, masked):
     (-10000 above the diagonal), sequence lengths for both kernels (direct up to 128 keys,
     staged from 160 to 512, including 160 and 192 where one 128-key chunk is partial),
     a partial last 64-query block (96, 160, 288) and no mask.
+    The unmasked cases use scale 1.0: scores of std ~2.7 give a peaked softmax, so the
+    output depends on which key each probability belongs to (at the BERT scale 0.125 an
+    unmasked softmax over U(-1, 1) inputs is nearly uniform and the output ~ mean(V)
+    whatever the key order).
     Tolerance 1e-2 + 1e-2 |ref| (P is rounded to the data type before P V)."""
     g = torch.Generator().manual_seed(b * 7 + s + heads)
     q = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
     k = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
     v = (torch.rand(b * heads, s, 64, generator=g) * 2 - 1).to(dtype)
     mask = torch.triu(torch.full((s, s), -10000.0), 1).to(dtype) if masked else None
-    want = O.attention_ref(q, k, v, b, 0.125, mask)
-    print(f"[parity] attention_fwd b={b} s={s} heads={heads} {dtype} masked={masked}", flush=True)
-    got = runtime.attention_fwd(q.cuda(), k.cuda(), v.transpose(1, 2).contiguous().cuda(), b, 0.125,
+    scale = 0.125 if masked else 1.0
+    want = O.attention_ref(q, k, v, b, scale, mask)
+    print(f"[parity] attention_fwd b={b} s={s} heads={heads} {dtype} masked={masked} scale={scale}", flush=True)
+    got = runtime.attention_fwd(q.cuda(), k.cuda(), v.transpose(1, 2).contiguous().cuda(), b, scale,
                                 mask.cuda() if mask is not None else None)
     torch.cuda.synchronize()
     _close(got.float().cpu(), want, 1e-2, 1e-2, f"attention b={b} s={s} {dtype}")

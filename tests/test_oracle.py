@@ -400,3 +400,34 @@ def test_bert_layer_ref_matches_sdpa_composition():
     want = F.layer_norm(inter @ D(w.output_kernel) + D(w.output_bias) + x1, (H,),
                         D(w.output_layernorm_gamma), D(w.output_layernorm_beta), 1e-5)
     torch.testing.assert_close(got.double(), want, rtol=1e-4, atol=1e-4)
+
+
+def test_attention_ref_matches_fp64_sdpa_and_loops():
+    """attention_ref against torch's fp64 scaled_dot_product_attention with the additive
+    causal mask, merged to [batch, seq, heads*d], and against explicit fp64 loops
+    (scores, row max, exp, normalise, weighted sum of v) for every (batch, head); the
+    scale is large enough that the softmax is peaked, so a key / value index slip shows."""
+    b, heads, s, d = 2, 3, 9, 5
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(b * heads, s, d, generator=g) for _ in range(3))
+    mask = torch.triu(torch.full((s, s), -10000.0), 1)
+    for m in (mask, None):
+        got = O.attention_ref(q, k, v, b, 0.9, m)
+        assert got.shape == (b, s, heads * d)
+        want = F.scaled_dot_product_attention(
+            q.double().reshape(b, heads, s, d), k.double().reshape(b, heads, s, d), v.double().reshape(b, heads, s, d),
+            attn_mask=m.double() if m is not None else None, scale=0.9)
+        torch.testing.assert_close(got.double(), want.permute(0, 2, 1, 3).reshape(b, s, heads * d),
+                                   rtol=1e-5, atol=1e-5)
+        Q, K, V = _np64(q), _np64(k), _np64(v)
+        Mk = _np64(m) if m is not None else np.zeros((s, s))
+        for bh in range(b * heads):
+            bi, hi = divmod(bh, heads)
+            for i in range(s):
+                z = [sum(Q[bh, i, t] * K[bh, j, t] for t in range(d)) * 0.9 + Mk[i, j] for j in range(s)]
+                zmax = max(z)
+                e = [math.exp(x - zmax) for x in z]
+                tot = sum(e)
+                for t in range(d):
+                    o = sum(e[j] / tot * V[bh, j, t] for j in range(s))
+                    assert abs(float(got[bi, i, hi * d + t]) - o) < 1e-5
