@@ -31,7 +31,7 @@ EXPORTED_SYMBOLS = (
     "icpp_layernorm_fwd", "icpp_layernorm_bwd_workspace_bytes", "icpp_layernorm_bwd", "icpp_softmax",
     "icpp_softmax_scaled_masked",
     "icpp_gemm_bias_residual_layernorm", "icpp_qkv_split_heads", "icpp_merge_heads", "icpp_attention_fwd",
-    "icpp_clock_probe", "icpp_gemm_noalloc",
+    "icpp_clock_probe", "icpp_gemm_noalloc", "icpp_read_probe",
 )
 CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
@@ -80,6 +80,7 @@ _SIGNATURES = {
     "icpp_merge_heads": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "icpp_clock_probe": (_i, [_vp, ctypes.c_double, _vp]),
     "icpp_gemm_noalloc": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp]),
+    "icpp_read_probe": (_i, [_vp, _sz, ctypes.c_uint, _i, _i, _i, _vp, _sz, _vp]),
 }
 
 
