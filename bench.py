@@ -118,19 +118,24 @@ def probe_reads():
     sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     rows = []
-    for (mib, ld, stripe, rpw, threads, what) in [
-            (16, 4096, 4096, 16, 1024, "64 KiB row blocks, 256 WGs"),
-            (16, 4096, 128, 512, 256, "128 B x 512-row stripes (split-K 8 over 32 column blocks), 256 WGs"),
-            (16, 4096, 64, 1024, 256, "64 B x 1024-row stripes, 256 WGs"),
-            (16, 4096, 16, 4096, 256, "16 B x 4096-row stripes (whole K per 16-column block), 256 WGs"),
-            (16, 4096, 4096, 256, 1024, "1 MiB row blocks, 16 WGs (per-CU rate)"),
-            (256, 4096, 4096, 256, 1024, "1 MiB row blocks, 256 WGs")]:
+    for (mib, ld, stripe, rpw, threads, passes, shared, what) in [
+            (16, 4096, 4096, 16, 1024, 1, 0, "64 KiB row blocks, 256 WGs"),
+            (16, 4096, 128, 512, 256, 1, 0, "128 B x 512-row stripes (split-K 8 over 32 column blocks), 256 WGs"),
+            (16, 4096, 64, 1024, 256, 1, 0, "64 B x 1024-row stripes, 256 WGs"),
+            (16, 4096, 16, 4096, 256, 1, 0, "16 B x 4096-row stripes (whole K per 16-column block), 256 WGs"),
+            (16, 4096, 4096, 256, 1024, 1, 0, "1 MiB row blocks, 16 WGs (per-CU HBM rate)"),
+            (16, 4096, 4096, 128, 1024, 1, 0, "512 KiB row blocks, 32 WGs"),
+            (16, 4096, 4096, 64, 1024, 1, 0, "256 KiB row blocks, 64 WGs"),
+            (256, 4096, 4096, 256, 1024, 1, 0, "1 MiB row blocks, 256 WGs"),
+            (16, 4096, 4096, 16, 1024, 16, 0, "64 KiB row blocks read 16 times (L2-resident after the first), 256 WGs"),
+            (16, 4096, 4096, 16, 1024, 16, 1, "one 64 KiB block read 16 times by all 256 WGs (shared hot lines)"),
+            (16, 4096, 4096, 16, 256, 16, 0, "64 KiB row blocks read 16 times, 256 threads per WG")]:
         nbytes = mib << 20
         windows = total // nbytes
 
         def launch(i):
             lib().call("icpp_read_probe", buf.data_ptr() + (i % windows) * nbytes, nbytes, ld, stripe, rpw, threads,
-                       sink.data_ptr(), sink.numel(), stream)
+                       passes, shared, sink.data_ptr(), sink.numel(), stream)
         for i in range(3):
             launch(i)
         torch.cuda.synchronize()
@@ -142,8 +147,11 @@ def probe_reads():
         e.record()
         torch.cuda.synchronize()
         us = s.elapsed_time(e) / reps * 1e3
-        rows.append({"pattern": what, "mib": mib, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1)})
-        print(f"[probe] {mib} MiB, {what}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+        moved = nbytes * passes  # bytes delivered to the CUs
+        rows.append({"pattern": what, "mib": mib, "passes": passes, "us": round(us, 2),
+                     "gbps": round(moved / us / 1e3, 1)})
+        print(f"[probe] {mib} MiB x {passes}, {what}: {us:.2f} us, {moved / us / 1e3:.0f} GB/s into the CUs",
+              file=sys.stderr, flush=True)
     return rows
 
 
@@ -240,12 +248,14 @@ def _load_traffic(workload: str):
         return None
 
 
-def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
+def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: int = -1):
     """Every benchmark configuration: tuned config, TFLOP/s, fraction of its roofline.
 
     ``fixed_configs``: the JSON an earlier ``--op`` run printed; its rows' configs
     are reused instead of tuning (profiler runs time what the plain run chose --
-    under a kernel tracer the tuner's own short timings are distorted)."""
+    under a kernel tracer the tuner's own short timings are distorted).
+    ``row_index`` >= 0 keeps only that row of the ``only`` selection (one row per
+    profiler run, so every dispatch in the run belongs to it)."""
     import torch
 
     from icpp_tuning_amd.autotuner.interface import benchmark_ms, tune
@@ -264,8 +274,17 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
             if "raw_config" in r:
                 fixed[(r["op"], json.dumps(r["shape"], sort_keys=True))] = r["raw_config"]
 
-    def record(op, desc, shape, flops, min_bytes, dtype, **extra):
+    seen = [0]
+
+    def selected(op) -> bool:
         if only and not op.startswith(only):
+            return False
+        i = seen[0]
+        seen[0] += 1
+        return row_index < 0 or i == row_index
+
+    def record(op, desc, shape, flops, min_bytes, dtype, **extra):
+        if not selected(op):
             return
         # Timed over input copies whose total exceeds the 256 MiB MALL + L2, so
         # every launch reads its operands from HBM, and tuned the same way: with one
@@ -333,7 +352,7 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
     from icpp_tuning_amd import runtime as RT
 
     def record_rows(op, shape, dtype, make, nbytes):
-        if only and not op.startswith(only):
+        if not selected(op):
             return
         copies = max(1, min(16, -(-(600 << 20) // max(1, nbytes))))
         runs = [make(i) for i in range(copies)]
@@ -377,7 +396,7 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = ""):
     # this library's GEMM blocks vs the same layer composed from torch ops, both on this GPU
     def record_bert(batch, seq, layers=12):
         op = "bert_base_e2e"
-        if only and not op.startswith(only):
+        if not selected(op):
             return
         import math as _m
         import torch.nn.functional as TF
@@ -567,6 +586,8 @@ def main():
                     help="per-op table only, for the ops whose name starts with this (e.g. conv2d, gemm_bias_layernorm)")
     ap.add_argument("--op-configs", default="",
                     help="with --op: reuse the configs of an earlier --op run's JSON instead of tuning")
+    ap.add_argument("--row-index", type=int, default=-1,
+                    help="with --op: run only this row (0-based) of the selected rows")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
     ap.add_argument("--probe-reads", action="store_true",
@@ -594,7 +615,7 @@ def main():
         print(json.dumps({"read_probe": probe_reads()}), flush=True)
         return 0
     if args.op:  # one family of per-op rows only (profiling runs)
-        print(json.dumps({"ops": bench_ops(args.quick, args.op, args.op_configs)}), flush=True)
+        print(json.dumps({"ops": bench_ops(args.quick, args.op, args.op_configs, args.row_index)}), flush=True)
         return 0
     head = headline(args)
     rows = None

@@ -80,7 +80,7 @@ _SIGNATURES = {
     "icpp_merge_heads": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "icpp_clock_probe": (_i, [_vp, ctypes.c_double, _vp]),
     "icpp_gemm_noalloc": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp]),
-    "icpp_read_probe": (_i, [_vp, _sz, ctypes.c_uint, _i, _i, _i, _vp, _sz, _vp]),
+    "icpp_read_probe": (_i, [_vp, _sz, ctypes.c_uint, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
 }
 
 

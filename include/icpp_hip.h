@@ -265,14 +265,17 @@ int icpp_clock_probe(unsigned long long* out, double seconds, void* stream);
 /*
  * Measurement aid, no counterpart in the reference: the read-bandwidth probe.  Reads
  * `bytes` of device memory viewed as rows of `ld` bytes, one workgroup of `threads`
- * (256 / 512 / 1024) per stripe of `stripe` bytes x `rows_per_wg` rows, 16 bytes per
+ * (256 / 512 / 1024, a multiple of stripe / 16) per stripe of `stripe` bytes x
+ * `rows_per_wg` rows, 16 bytes per
  * lane per load, 8 loads in flight per lane; neighbouring stripes share an XCD.
- * Time it with events to get the bandwidth a partition pattern sustains (the
- * workgroup count is (ld / stripe) * (bytes / ld / rows_per_wg) <= sink_ints; sink is
- * a device int array that is written only in a sentinel case).
+ * Each workgroup reads its stripe `passes` times (1-64; later passes hit L2), and
+ * with `shared` non-zero every workgroup reads stripe 0 (the same lines).  Time it
+ * with events to get the bandwidth a partition pattern sustains (the workgroup
+ * count is (ld / stripe) * (bytes / ld / rows_per_wg) <= sink_ints; sink is a device
+ * int array that is written only in a sentinel case).
  */
 int icpp_read_probe(const void* base, size_t bytes, unsigned ld, int stripe, int rows_per_wg, int threads,
-                    int* sink, size_t sink_ints, void* stream);
+                    int passes, int shared, int* sink, size_t sink_ints, void* stream);
 
 #ifdef __cplusplus
 }
