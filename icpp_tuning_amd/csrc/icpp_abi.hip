@@ -69,13 +69,16 @@ int check_launch(hipError_t e, const char* what) {
 hipError_t launch_splitk_reduce(int dt, const float* ws, void* C, const void* bias, int M, int N, int ldc,
                                 int splits, float alpha, int act, hipStream_t s, ConvEpiArgs ce = ConvEpiArgs{}) {
   const size_t groups = (size_t)M * (N / 4);
-  const int blocks = (int)std::min<size_t>((groups + 255) / 256, 4096);
+  // small outputs (skinny-M decode rows) spread over one-wave workgroups, so that more
+  // CUs issue the partial loads: a CU's request rate, not HBM, bounds a grid this small
+  const int threads = groups < (size_t)256 * 512 ? 64 : 256;
+  const int blocks = (int)std::min<size_t>((groups + threads - 1) / threads, 4096);
   if (dt == DT_F16)
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_F16>, dim3(blocks), dim3(threads), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
   else if (dt == DT_BF16)
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_BF16>, dim3(blocks), dim3(threads), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
   else
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT_FP8>, dim3(blocks), dim3(256), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT_FP8>, dim3(blocks), dim3(threads), 0, s, ws, C, bias, M, N, ldc, splits, alpha, act, ce);
   return hipGetLastError();
 }
 

@@ -423,8 +423,20 @@ __device__ __forceinline__ void splitk_group(const float* ws, void* C, const voi
                                              int splits, float alpha, int act, const ConvEpiArgs& ce, int m, int n) {
   typedef typename DTraits<DT>::OutT OutT;
   typedef typename DTraits<DT>::BiasT BiasT;
+  // All of a group's partial loads go out before the first add (8 at a time), so the
+  // slices cost one memory round trip instead of one each; the sum stays in slice order.
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int z = 0; z < splits; ++z) s += Vec4Store<float>::ld(ws + ((size_t)z * M + m) * N + n);
+  const size_t zstride = (size_t)M * N;
+  const float* w = ws + (size_t)m * N + n;
+  for (int z0 = 0; z0 < splits; z0 += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < splits) v[u] = Vec4Store<float>::ld(w + (size_t)(z0 + u) * zstride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (z0 + u < splits) s += v[u];
+  }
   if (ce.flags != 0) {
     f32x4 sc, sh;
     conv_bn4<BiasT>(ce, N, n, sc, sh);
