@@ -248,6 +248,16 @@ def _load_traffic(workload: str):
         return None
 
 
+def table_seed(desc, **shape):
+    """The shipped measured database's pick for this shape (the adaptive tuner's
+    level 1), measured by the tuner next to the formula's ranking; [] when the
+    shape lies outside every profiled range."""
+    from icpp_tuning_amd.autotuner.perfdb import AdaptiveTuner
+
+    r = AdaptiveTuner(desc).select(**shape)
+    return [r.config] if r.level == "table" else []
+
+
 def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: int = -1):
     """Every benchmark configuration: tuned config, TFLOP/s, fraction of its roofline.
 
@@ -295,7 +305,8 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
         hbm_bound = flops / min_bytes < peak * 1e3 / HBM_GBPS
         given = fixed.get((op, json.dumps(shape, sort_keys=True)))
         res = None if given is not None else tune(desc, top_k=top_k, warmup=2, reps=10, budget_ms=60.0,
-                                                  input_copies=copies, **shape)
+                                                  input_copies=copies, seed_configs=table_seed(desc, **shape),
+                                                  **shape)
         best = given if given is not None else res.best_config
         sets = [desc.make_inputs(**shape) for _ in range(copies)]
         runs = [desc.make_runner(best, inp, **shape) for inp in sets]
@@ -317,7 +328,9 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
                 "formula_top1_ms": round(res.formula_top1_ms, 5),
                 "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),
                           "compile_s": round(res.compile_s, 4), "bench_s": round(res.bench_s, 3),
-                          "candidates": len(res.candidates), "n_configs": res.n_configs, "n_pruned": res.n_pruned}})
+                          "candidates": len(res.candidates), "n_configs": res.n_configs, "n_pruned": res.n_pruned,
+                          "best_from": "table" if any(c["seed"] and c["config"] == best for c in res.candidates)
+                          else "formula"}})
         row.update(extra)
         rows.append(row)
         how = f"tuned in {res.time_to_best_s:.2f}s" if res is not None else "config given"
@@ -518,7 +531,8 @@ def headline(args):
     else:
         # 30 launches per timed batch (~3.5 ms): shorter bursts run at a boost clock the
         # steady state does not keep, and flip the choice between near-equal tiles
-        tuned = tune(desc, top_k=4, warmup=5, reps=30, input_copies="auto", M=M, N=N, K=K)
+        tuned = tune(desc, top_k=4, warmup=5, reps=30, input_copies="auto",
+                     seed_configs=table_seed(desc, M=M, N=N, K=K), M=M, N=N, K=K)
         cfg = tuned.best_config
     kern = GBA.build_kernel(M, N, K, config=cfg, act="gelu_tanh", dtype="bf16")
     set_bytes = 2 * (M * K + K * N + M * N + N)
@@ -561,7 +575,9 @@ def headline(args):
                         "compile_s": round(tuned.compile_s, 4), "bench_s": round(tuned.bench_s, 3),
                         "formula_top1": desc.format_config(tuned.formula_top1),
                         "formula_top1_ms": round(tuned.formula_top1_ms, 5), "select_best_s": round(select_s, 4),
-                        "candidates": len(tuned.candidates)}
+                        "candidates": len(tuned.candidates),
+                        "best_from": "table" if any(c["seed"] and c["config"] == cfg for c in tuned.candidates)
+                        else "formula"}
     print(f"[bench] headline {workload} {roof['kernel_us']} us/launch, {achieved:.1f} TFLOP/s "
           f"({100 * roof['frac']:.1f}% of peak), sclk {sclk and round(sclk)} MHz, "
           f"{copies} input copies", file=sys.stderr, flush=True)

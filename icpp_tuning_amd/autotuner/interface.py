@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Any, Callable, Dict, List, Optional, Tuple, Union
+from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple, Union
 
 from .cost_model import OpSpec, TuneConfig, score_formula, score_formula_detailed
 from .gpu_spec import GPUSpec, get_gpu_spec
@@ -210,12 +210,15 @@ def input_bytes(inputs: Any) -> int:
 
 def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: int = 4, warmup: int = 2,
          reps: int = 5, budget_ms: float = 0.0, prune: bool = True, input_copies: Union[int, str] = 1,
-         **shape_kwargs: Any) -> TuneResult:
+         seed_configs: Sequence[Dict[str, Any]] = (), **shape_kwargs: Any) -> TuneResult:
     """Formula-rank, then measure candidates on the device and keep the fastest.
 
     The formula's top_k are always measured.  With ``budget_ms`` the search goes
     on down the ranking while the device time spent measuring stays within the
     budget, so cheap (small) problems get a wider search than large ones.
+    ``seed_configs`` (e.g. the measured database's pick for the shape, the
+    design's warm start) are measured first, in addition to the ranking; a seed
+    the descriptor does not offer for the shape is skipped.
     ``prune=False`` ranks (and, with a large top_k, measures) the whole compiled
     set for the shape, as offline profiling does.  ``input_copies`` > 1 times
     every candidate round-robin over that many input sets, so an operand set
@@ -249,22 +252,34 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     cands = []
     spent_ms = 0.0
     launches = max(warmup, 1) + 3 * reps + reps       # warmup + 3 timed batches + graph capture
-    for rank, e in enumerate(ranked):
-        if rank >= top_k and spent_ms >= budget_ms:
-            break
+
+    def measure(raw, formatted, score, seed):
+        nonlocal compile_s, spent_ms
         tc = time.perf_counter()
-        runs = [descriptor.make_runner(e["raw_config"], inp, **shape_kwargs) for inp in inputs]
+        runs = [descriptor.make_runner(raw, inp, **shape_kwargs) for inp in inputs]
         compile_s += time.perf_counter() - tc
         ms = benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
         spent_ms += ms * launches
-        cands.append({"config": e["raw_config"], "formatted": e["formatted"], "score": e["score"], "ms": ms,
-                      "tflops": flops / ms / 1e9})
+        cands.append({"config": raw, "formatted": formatted, "score": score, "ms": ms,
+                      "tflops": flops / ms / 1e9, "seed": seed})
+
+    seeds = [c for c in seed_configs if c in all_cfgs]
+    for c in seeds:
+        measure(c, descriptor.format_config(c), None, True)
+    for rank, e in enumerate(ranked):
+        if rank >= max(1, top_k) and spent_ms >= budget_ms:
+            break
+        if e["raw_config"] in seeds:
+            continue
+        measure(e["raw_config"], e["formatted"], e["score"], False)
     t2 = t_in + compile_s
     t3 = time.perf_counter()
     best = min(cands, key=lambda c: c["ms"])
+    top1 = ranked[0]["raw_config"]
+    top1_ms = next(c["ms"] for c in cands if c["config"] == top1)
     return TuneResult(
         best_config=best["config"], best_ms=best["ms"], best_tflops=best["tflops"],
-        formula_top1=cands[0]["config"], formula_top1_ms=cands[0]["ms"], candidates=cands,
+        formula_top1=top1, formula_top1_ms=top1_ms, candidates=cands,
         prune_rank_s=t1 - t0, compile_s=t2 - t_in, bench_s=t3 - t2, time_to_best_s=(t3 - t0) - (t_in - t1),
         n_configs=len(all_cfgs), n_pruned=len(all_cfgs) - len(ranked), inputs_s=t_in - t1)
 

@@ -457,6 +457,19 @@ __device__ __forceinline__ void splitk_group(const float* ws, void* C, const voi
 // ---------------------------------------------------------------------------
 // The mainloop + epilogue kernel
 // ---------------------------------------------------------------------------
+// The A_HALO input halo: an LDS array in the kernels that use it, none in the others.
+template <bool ON, int N>
+struct HaloLds {
+  static __device__ __forceinline__ char ICPP_LDS* ptr() {
+    __shared__ __attribute__((aligned(16))) char halo[N];
+    return (char ICPP_LDS*)halo;
+  }
+};
+template <int N>
+struct HaloLds<false, N> {
+  static __device__ __forceinline__ char ICPP_LDS* ptr() { return nullptr; }
+};
+
 template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int STAGES, int EPI, int ALOAD>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_kernel(KArgs p) {
@@ -488,7 +501,8 @@ gemm_kernel(KArgs p) {
   __shared__ __attribute__((aligned(16))) char lds1[STAGES > 1 ? SBYTES : 16];
   __shared__ __attribute__((aligned(16))) char lds2[STAGES > 2 ? SBYTES : 16];
   __shared__ __attribute__((aligned(16))) char lds3[STAGES > 3 ? SBYTES : 16];
-  __shared__ __attribute__((aligned(16))) char halo_lds[HALO ? HALO_CAP : 16];
+  // the halo array exists only in A_HALO kernels, so four 40 KiB stages fill the 160 KiB exactly
+  char ICPP_LDS* const halo_lds = HaloLds<HALO, HALO_CAP>::ptr();
   static_assert(!HALO || (G::ESZ == 2 && BK == 64), "A_HALO: 16-bit data, one 64-channel chunk per pixel");
   static_assert(!HALO || SBYTES * STAGES + HALO_CAP <= 160 * 1024, "A_HALO: LDS overflow");
   auto stage_base = [&](auto S) -> char ICPP_LDS* ICPP_INLINE {

