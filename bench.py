@@ -458,6 +458,82 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
     return rows
 
 
+def vs_libraries():
+    """This library's tuned config (tune() as the per-op rows run it: the
+    formula's ranking measured, seeded with the shipped database's pick) against
+    the same op composed from torch calls (hipBLASLt GEMMs, MIOpen convolution, torch elementwise and
+    LayerNorm kernels), both timed over the same rotated input copies (larger
+    than the MALL).  For each conv shape, the dense GEMM of the same M x N x K
+    is timed too (this library's pick and torch.mm), which separates the cost of
+    the gather from the cost of the GEMM shape."""
+    import torch
+    import torch.nn.functional as F
+
+    from icpp_tuning_amd.autotuner.interface import benchmark_ms, input_bytes, tune
+    from icpp_tuning_amd.kernels import conv2d as CV
+    from icpp_tuning_amd.kernels import fp8_gemm_bias_act as F8
+    from icpp_tuning_amd.kernels import gemm as G
+    from icpp_tuning_amd.kernels import gemm_bias_act as GBA
+    from icpp_tuning_amd.kernels import gemm_bias_layernorm as LN
+
+    rows = []
+
+    def one(op, desc, shape, flops, torch_name, torch_fn, prep=None):
+        sets = [desc.make_inputs(**shape)]
+        copies = max(1, min(16, -(-(600 << 20) // max(1, input_bytes(sets[0])))))
+        sets += [desc.make_inputs(**shape) for _ in range(copies - 1)]
+        cfg = tune(desc, top_k=4, warmup=2, reps=10, budget_ms=60.0, input_copies=copies,
+                   seed_configs=table_seed(desc, **shape), **shape).best_config
+        runs = [desc.make_runner(cfg, d, **shape) for d in sets]
+        reps = max(20, 2 * copies)
+        ours = benchmark_ms(runs, warmup=copies, reps=reps)
+        row = {"op": op, "shape": shape, "config": desc.format_config(cfg), "us": round(ours * 1e3, 2),
+               "tflops": round(flops / ours / 1e9, 1), "torch": torch_name, "input_copies": copies}
+        try:
+            extra = [prep(d) if prep else d for d in sets]
+            t = benchmark_ms([(lambda d=d: torch_fn(d)) for d in extra], warmup=copies, reps=reps)
+            row.update({"torch_us": round(t * 1e3, 2), "speedup": round(t / ours, 3)})
+        except Exception as e:  # a torch path this image's build does not offer
+            row.update({"torch_us": None, "torch_error": f"{type(e).__name__}: {str(e)[:120]}"})
+        rows.append(row)
+        print(f"[vs] {op} {shape}: {row['us']} us ({row['config']}) vs {torch_name} {row.get('torch_us')} us",
+              file=sys.stderr, flush=True)
+        del sets, runs
+        torch.cuda.empty_cache()
+
+    M = N = K = 1024
+    one("gemm", G.DESCRIPTOR, dict(M=M, N=N, K=K), 2.0 * M * N * K, "mm",
+        lambda d: torch.mm(d["A"], d["B"], out=d["C"]))
+    M = N = K = 4096
+    one("gemm_bias_gelu_tanh", GBA.descriptor("gelu_tanh", "bf16"), dict(M=M, N=N, K=K), 2.0 * M * N * K,
+        "addmm + gelu(tanh)", lambda d: F.gelu(torch.addmm(d["bias"], d["A"], d["B"]), approximate="tanh"))
+    for N in (768, 1024, 4096):
+        M, K = 8192, 4096
+        one("gemm_bias_layernorm", LN.DESCRIPTOR, dict(M=M, N=N, K=K), 2.0 * M * N * K, "addmm + layer_norm",
+            lambda d, N=N: F.layer_norm(torch.addmm(d["bias"], d["A"], d["B"]), (N,), d["gamma"], d["beta"]))
+    for (Nb, H, W, C, Fo) in ((32, 56, 56, 64, 64), (32, 14, 14, 256, 256), (32, 7, 7, 512, 512)):
+        shape = dict(N=Nb, C=C, H=H, W=W, OC=Fo, KH=3, KW=3, stride=1, padding=1)
+        Mg, Kg = Nb * H * W, 9 * C
+        fl = 2.0 * Mg * Fo * Kg
+        one("conv2d", CV.DESCRIPTOR, shape, fl, "conv2d (MIOpen, channels-last)",
+            lambda d: F.conv2d(d["Xc"], d["Wc"], padding=1),
+            prep=lambda d: {"Xc": d["X"].permute(0, 3, 1, 2),
+                            "Wc": d["W"].permute(3, 0, 1, 2).contiguous().permute(0, 3, 1, 2)})
+        one("gemm (conv's M x N x K)", G.DESCRIPTOR, dict(M=Mg, N=Fo, K=Kg), fl, "mm",
+            lambda d: torch.mm(d["A"], d["B"], out=d["C"]))
+    for (M, N, K) in ((16, 4096, 4096), (256, 4096, 4096), (4096, 4096, 4096)):
+        def f8(d):
+            y = torch._scaled_mm(d["A"], d["Bt"].t(), scale_a=d["sa"], scale_b=d["sb"], bias=d["bias16"],
+                                 out_dtype=torch.bfloat16)
+            return F.silu(y)
+        one("fp8_gemm_bias_silu", F8.DESCRIPTOR, dict(M=M, N=N, K=K), 2.0 * M * N * K, "_scaled_mm + silu", f8,
+            prep=lambda d: {"A": d["A"], "Bt": d["B"].t().contiguous(),
+                            "sa": torch.tensor(float(d["scale_a"]), device="cuda"),
+                            "sb": torch.tensor(float(d["scale_b"]), device="cuda"),
+                            "bias16": d["bias"].to(torch.bfloat16)})
+    return rows
+
+
 def _shape_str(shape) -> str:
     if isinstance(shape, dict):
         if "OC" in shape:
@@ -606,6 +682,8 @@ def main():
                     help="with --op: run only this row (0-based) of the selected rows")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
+    ap.add_argument("--vs-libraries", action="store_true",
+                    help="print this library's picks against the same ops composed from torch calls and exit")
     ap.add_argument("--probe-reads", action="store_true",
                     help="print the read bandwidth of the kernels' partition patterns (icpp_read_probe) and exit")
     args = ap.parse_args()
@@ -629,6 +707,9 @@ def main():
         return 0
     if args.probe_reads:
         print(json.dumps({"read_probe": probe_reads()}), flush=True)
+        return 0
+    if args.vs_libraries:
+        print(json.dumps({"vs_libraries": vs_libraries()}), flush=True)
         return 0
     if args.op:  # one family of per-op rows only (profiling runs)
         print(json.dumps({"ops": bench_ops(args.quick, args.op, args.op_configs, args.row_index)}), flush=True)

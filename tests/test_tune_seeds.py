@@ -53,3 +53,29 @@ def test_seed_not_offered_for_the_shape_is_skipped(fake_device):
     bad = dict(rank_all(d, MI355X, **SHAPE)[0]["raw_config"], block_K=48)  # no compiled instance
     r = tune(d, MI355X, top_k=2, seed_configs=[bad], **SHAPE)
     assert all(not c["seed"] for c in r.candidates) and len(r.candidates) == 2
+
+
+def test_first_timing_discarded_and_two_fastest_retimed(monkeypatch, fake_device):
+    """Timings drift down over the search (a clock ramping up): the first
+    timing is thrown away, and the winner is decided on the mean of two
+    timings of the two fastest, not on one lucky timing."""
+    d = fake_device
+    calls = []
+
+    def drifting(run, **kw):
+        calls.append(run)
+        base = 1.0 / (run["block_M"] * run["block_N"])
+        return base * (1.0 + 0.5 / len(calls))  # later calls read faster
+
+    monkeypatch.setattr(interface, "benchmark_ms", drifting)
+    r = tune(d, MI355X, top_k=4, **SHAPE)
+    n = len(r.candidates)
+    assert len(calls) == 1 + n + 2
+    assert calls[0] == calls[1] == r.candidates[0]["config"]       # warm-up timing, then the real one
+    retimed = [c for c in r.candidates if "ms_again" in c]
+    assert len(retimed) == 2
+    fastest_two = sorted(r.candidates, key=lambda c: c["ms"])[:2]
+    assert {c["formatted"] for c in retimed} == {c["formatted"] for c in fastest_two}
+    win = min(retimed, key=lambda c: c["ms"] + c["ms_again"])
+    assert r.best_config == win["config"]
+    assert r.best_ms == pytest.approx((win["ms"] + win["ms_again"]) / 2)
