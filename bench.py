@@ -314,6 +314,8 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
         best = given if given is not None else res.best_config
         sets = [desc.make_inputs(**shape) for _ in range(copies)]
         runs = [desc.make_runner(best, inp, **shape) for inp in sets]
+        # the device idled while the inputs were built: a first timing settles its clock
+        benchmark_ms(runs, warmup=copies, reps=max(20, 2 * copies))
         ms = benchmark_ms(runs, warmup=copies, reps=max(20, 2 * copies))
         del sets, runs
         tflops = flops / ms / 1e9
@@ -490,6 +492,7 @@ def vs_libraries():
                    seed_configs=table_seed(desc, **shape), **shape).best_config
         runs = [desc.make_runner(cfg, d, **shape) for d in sets]
         reps = max(20, 2 * copies)
+        benchmark_ms(runs, warmup=copies, reps=reps)  # settles the clock after the idle input build
         ours = benchmark_ms(runs, warmup=copies, reps=reps)
         row = {"op": op, "shape": shape, "config": desc.format_config(cfg), "us": round(ours * 1e3, 2),
                "tflops": round(flops / ours / 1e9, 1), "torch": torch_name, "input_copies": copies}
