@@ -334,7 +334,8 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
                 "formula_top1_ms": round(res.formula_top1_ms, 5),
                 "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),
                           "compile_s": round(res.compile_s, 4), "bench_s": round(res.bench_s, 3),
-                          "candidates": len(res.candidates), "n_configs": res.n_configs, "n_pruned": res.n_pruned,
+                          "candidates": len(res.candidates), "failed": len(res.failed),
+                          "n_configs": res.n_configs, "n_pruned": res.n_pruned,
                           "best_from": "table" if any(c["seed"] and c["config"] == best for c in res.candidates)
                           else "formula"}})
         row.update(extra)

@@ -21,6 +21,7 @@ import time
 from dataclasses import dataclass, field
 from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple, Union
 
+from .._lib import IcppCallError
 from .cost_model import OpSpec, TuneConfig, score_formula, score_formula_detailed
 from .gpu_spec import GPUSpec, get_gpu_spec
 
@@ -148,6 +149,7 @@ class TuneResult:
     n_configs: int = 0
     n_pruned: int = 0
     inputs_s: float = 0.0   # synthetic input generation (excluded from time_to_best)
+    failed: List[Dict[str, Any]] = field(default_factory=list)  # candidates dropped, with the reason
 
     def as_dict(self) -> Dict[str, Any]:
         return dict(self.__dict__)
@@ -256,17 +258,24 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     launches = max(warmup, 1) + 3 * reps + reps       # warmup + 3 timed batches + graph capture
 
     runners = {}
+    failed = []
 
     def measure(raw, formatted, score, seed):
         nonlocal compile_s, spent_ms
-        tc = time.perf_counter()
-        runs = [descriptor.make_runner(raw, inp, **shape_kwargs) for inp in inputs]
-        compile_s += time.perf_counter() - tc
+        try:
+            tc = time.perf_counter()
+            runs = [descriptor.make_runner(raw, inp, **shape_kwargs) for inp in inputs]
+            compile_s += time.perf_counter() - tc
+            if not cands:
+                # the first timing after an idle device absorbs the clock ramp-up: discard it
+                benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
+            ms = benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
+        except (IcppCallError, ValueError) as e:
+            # a candidate the library or the launcher rejects is dropped with its reason
+            # (the reference's harness records "ERROR" rows and goes on, conv2d.py:453-460)
+            failed.append({"config": raw, "formatted": formatted, "error": f"{type(e).__name__}: {e}"})
+            return
         runners[formatted] = runs
-        if not cands:
-            # the first timing after an idle device absorbs the clock ramp-up: discard it
-            benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
-        ms = benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
         spent_ms += ms * launches
         cands.append({"config": raw, "formatted": formatted, "score": score, "ms": ms,
                       "tflops": flops / ms / 1e9, "seed": seed})
@@ -285,6 +294,9 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     for c in sorted(cands, key=lambda c: c["ms"])[:2][::-1] if len(cands) > 1 else ():
         runs = runners[c["formatted"]]
         c["ms_again"] = benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
+    if not cands:
+        raise RuntimeError(f"{descriptor.name}: every measured candidate failed for {shape_kwargs}: "
+                           + "; ".join(f"{f['formatted']}: {f['error']}" for f in failed[:4]))
     t2 = t_in + compile_s
     t3 = time.perf_counter()
     best = min(cands, key=lambda c: (c["ms"] + c.get("ms_again", c["ms"])) / 2 if "ms_again" in c else float("inf"))
@@ -292,10 +304,10 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
         best = dict(best, ms=(best["ms"] + best["ms_again"]) / 2)
         best["tflops"] = flops / best["ms"] / 1e9
     top1 = ranked[0]["raw_config"]
-    top1_ms = next(c["ms"] for c in cands if c["config"] == top1)
+    top1_ms = next((c["ms"] for c in cands if c["config"] == top1), float("nan"))
     return TuneResult(
         best_config=best["config"], best_ms=best["ms"], best_tflops=best["tflops"],
-        formula_top1=top1, formula_top1_ms=top1_ms, candidates=cands,
+        formula_top1=top1, formula_top1_ms=top1_ms, candidates=cands, failed=failed,
         prune_rank_s=t1 - t0, compile_s=t2 - t_in, bench_s=t3 - t2, time_to_best_s=(t3 - t0) - (t_in - t1),
         n_configs=len(all_cfgs), n_pruned=len(all_cfgs) - len(ranked), inputs_s=t_in - t1)
 

@@ -79,3 +79,29 @@ def test_first_timing_discarded_and_two_fastest_retimed(monkeypatch, fake_device
     win = min(retimed, key=lambda c: c["ms"] + c["ms_again"])
     assert r.best_config == win["config"]
     assert r.best_ms == pytest.approx((win["ms"] + win["ms_again"]) / 2)
+
+
+def test_failing_candidate_is_dropped_with_its_reason(monkeypatch, fake_device):
+    """A candidate the library rejects (here: the runner raises the library's call
+    error) is dropped from the ranking with the reason recorded, and the search
+    goes on; when every candidate fails the search raises."""
+    from icpp_tuning_amd._lib import IcppCallError
+
+    d = fake_device
+    ranked = rank_all(d, MI355X, **SHAPE)
+    bad = ranked[1]["raw_config"]
+
+    def runner(raw, inp, **shape):
+        if raw == bad:
+            raise IcppCallError("icpp_gemm", -3, "injected: LDS overflow")
+        return raw
+
+    monkeypatch.setattr(d, "make_runner", runner)
+    r = tune(d, MI355X, top_k=4, **SHAPE)
+    assert [f["config"] for f in r.failed] == [bad]
+    assert "injected" in r.failed[0]["error"]
+    assert bad not in [c["config"] for c in r.candidates] and len(r.candidates) == 3
+
+    monkeypatch.setattr(d, "make_runner", lambda raw, inp, **shape: (_ for _ in ()).throw(ValueError("no")))
+    with pytest.raises(RuntimeError, match="every measured candidate failed"):
+        tune(d, MI355X, top_k=2, **SHAPE)
