@@ -1,0 +1,128 @@
+"""The C ABI's host code under AddressSanitizer (CPU only, no device work).
+
+icpp_tuning_amd/build_asan.py builds the library with ASan on the host pass
+(two instances, every hand-written translation unit).  A child process preloads
+the ASan runtime, loads that library and drives every entry point through its
+queries, argument checks and error paths (the paths a caller reaches before any
+launch), including long error messages and out-of-range instance indices.  The
+test fails on any ASan report or on an entry point that accepts an invalid call.
+"""
+
+import os
+import subprocess
+import sys
+import textwrap
+
+import pytest
+
+DRIVER = textwrap.dedent(r"""
+    import ctypes, sys
+    L = ctypes.CDLL(sys.argv[1])
+    vp, i, f, sz, d = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_double
+
+    class Tile(ctypes.Structure):
+        _fields_ = [(n, ctypes.c_int) for n in ("family", "dtype", "block_m", "block_n", "block_k", "waves_m",
+                    "waves_n", "stages", "mfma_m", "mfma_n", "mfma_k", "lds_bytes", "threads")] + \
+                   [("name", ctypes.c_char * 96)]
+
+    def fn(name, res, *args):
+        g = getattr(L, name)
+        g.restype = res
+        g.argtypes = list(args)
+        return g
+
+    last = fn("icpp_last_error", ctypes.c_char_p)
+    bad = []
+
+    def must_fail(name, rc):
+        msg = last()
+        if rc == 0 or not msg:
+            bad.append(f"{name}: rc {rc}, message {msg!r}")
+
+    assert fn("icpp_abi_version", i)() > 0
+    num = fn("icpp_num_instances", i, i)
+    info = fn("icpp_instance_info", i, i, i, ctypes.POINTER(Tile))
+    assert num(0) == 1, num(0)
+    t = Tile()
+    assert info(0, 0, ctypes.byref(t)) == 0 and t.name.decode().startswith("gemm_f16_64x64x64")
+    for fam, idx in ((0, 1), (0, -1), (0, 1 << 30), (-1, 0), (99, 0)):
+        must_fail("icpp_instance_info", info(fam, idx, ctypes.byref(t)))
+    must_fail("icpp_instance_info(null)", info(0, 0, None))
+    for fam in (-1, 99, 1 << 30):
+        must_fail("icpp_num_instances", num(fam))
+    ws = fn("icpp_workspace_bytes", sz, i, i, i, i, i, i)
+    assert ws(0, 0, 1024, 1024, 1024, 4) == 4 * 1024 * 1024 * 4
+    for a in ((0, 7, 64, 64, 64, 2), (0, -1, 64, 64, 64, 2), (42, 0, 64, 64, 64, 2), (0, 0, -5, 64, 64, 2)):
+        ws(*a)  # any value; must not read out of bounds
+    P = ctypes.c_void_p(16)  # never dereferenced: every call below fails its checks first
+    gemm = fn("icpp_gemm", i, i, vp, vp, vp, vp, i, i, i, i, i, i, i, f, f, i, vp, sz, vp)
+    must_fail("icpp_gemm inst", gemm(5, P, P, None, P, 64, 64, 64, 64, 64, 64, 0, 1.0, 1.0, 1, None, 0, None))
+    must_fail("icpp_gemm null", gemm(0, None, P, None, P, 64, 64, 64, 64, 64, 64, 0, 1.0, 1.0, 1, None, 0, None))
+    must_fail("icpp_gemm shape", gemm(0, P, P, None, P, 64, 60, 64, 64, 60, 60, 0, 1.0, 1.0, 1, None, 0, None))
+    must_fail("icpp_gemm act", gemm(0, P, P, None, P, 64, 64, 64, 64, 64, 64, 77, 1.0, 1.0, 1, None, 0, None))
+    must_fail("icpp_gemm split ws", gemm(0, P, P, None, P, 64, 64, 1024, 1024, 64, 64, 0, 1.0, 1.0, 4, None, 0,
+                                         None))
+    big = (1 << 31) - 1
+    must_fail("icpp_gemm huge", gemm(0, P, P, None, P, big, big, big, big, big, big, 0, 1.0, 1.0, big, None, 0, None))
+    noalloc = fn("icpp_gemm_noalloc", i, i, vp, vp, vp, vp, i, i, i, i, i, i, i, f, f, i, vp)
+    must_fail("icpp_gemm_noalloc scratch", noalloc(0, P, P, None, P, 4096, 4096, 4096, 4096, 4096, 4096, 0, 1.0, 1.0,
+                                                   64, None))
+    ln = fn("icpp_gemm_bias_layernorm", i, i, i, vp, vp, vp, vp, vp, vp, i, i, i, f, vp, sz, vp)
+    must_fail("icpp_gemm_bias_layernorm family", ln(9, 0, P, P, P, P, P, P, 64, 64, 64, 1e-5, None, 0, None))
+    must_fail("icpp_gemm_bias_layernorm inst", ln(1, 3, P, P, P, P, P, P, 64, 64, 64, 1e-5, None, 0, None))
+    rln = fn("icpp_gemm_bias_residual_layernorm", i, i, i, vp, vp, vp, vp, vp, vp, vp, i, i, i, f, vp, sz, vp)
+    must_fail("icpp_gemm_bias_residual_layernorm", rln(0, 0, P, P, P, P, P, P, P, 64, 60, 64, 1e-5, None, 0, None))
+    conv = fn("icpp_conv2d_nhwc", i, i, vp, vp, vp, i, i, i, i, i, i, i, i, i, i, i, vp, sz, vp)
+    must_fail("icpp_conv2d_nhwc inst", conv(3, P, P, P, 1, 8, 8, 64, 64, 3, 3, 1, 1, 1, 1, None, 0, None))
+    must_fail("icpp_conv2d_nhwc C%8", conv(0, P, P, P, 1, 8, 8, 60, 64, 3, 3, 1, 1, 1, 1, None, 0, None))
+    must_fail("icpp_conv2d_nhwc null", conv(0, None, P, P, 1, 8, 8, 64, 64, 3, 3, 1, 1, 1, 1, None, 0, None))
+    convf = fn("icpp_conv2d_nhwc_fused", i, i, vp, vp, vp, vp, vp, vp, vp, vp, f, i, i, i, i, i, i, i, i, i, i, i,
+               i, i, vp, sz, vp)
+    must_fail("icpp_conv2d_nhwc_fused flags", convf(0, P, P, P, None, None, None, None, None, 1e-5, 64, 0, 1, 8, 8,
+                                                    64, 64, 3, 3, 1, 1, 1, 1, None, 0, None))
+    lnf = fn("icpp_layernorm_fwd", i, i, vp, vp, vp, vp, vp, vp, i, i, i, i, f, vp)
+    must_fail("icpp_layernorm_fwd dtype", lnf(7, P, P, P, P, None, None, 4, 64, 64, 64, 1e-5, None))
+    must_fail("icpp_layernorm_fwd N", lnf(0, P, P, P, P, None, None, 4, 1 << 24, 1 << 24, 1 << 24, 1e-5, None))
+    must_fail("icpp_layernorm_fwd eps", lnf(0, P, P, P, P, None, None, 4, 64, 64, 64, -1.0, None))
+    lbw = fn("icpp_layernorm_bwd_workspace_bytes", sz, i, i, i, i)
+    assert lbw(0, 4, 1 << 24, 1 << 24) == 0 and lbw(0, -1, 64, 64) == 0
+    lb = fn("icpp_layernorm_bwd", i, i, vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, vp, sz, vp)
+    must_fail("icpp_layernorm_bwd ws", lb(0, P, P, P, P, P, P, P, P, 64, 256, 256, None, 0, None))
+    sm = fn("icpp_softmax", i, i, vp, vp, i, i, i, i, vp)
+    must_fail("icpp_softmax ld", sm(0, P, P, 4, 64, 32, 64, None))
+    smm = fn("icpp_softmax_scaled_masked", i, i, vp, vp, vp, f, i, i, i, i, i, vp)
+    must_fail("icpp_softmax_scaled_masked", smm(0, P, P, P, 0.125, 4, 64, 64, 64, 0, None))
+    qkv = fn("icpp_qkv_split_heads", i, i, vp, vp, vp, vp, vp, i, i, i, i, i, vp)
+    must_fail("icpp_qkv_split_heads", qkv(0, P, None, P, P, P, 1, 32, 12, 63, 0, None))
+    mh = fn("icpp_merge_heads", i, i, vp, vp, i, i, i, i, vp)
+    must_fail("icpp_merge_heads", mh(0, P, P, 1, 32, 12, 0, None))
+    att = fn("icpp_attention_fwd", i, i, vp, vp, vp, vp, f, vp, i, i, i, i, vp)
+    must_fail("icpp_attention_fwd", att(0, P, P, P, None, 0.125, P, 1, 33, 12, 64, None))
+    clk = fn("icpp_clock_probe", i, ctypes.POINTER(ctypes.c_ulonglong), d, vp)
+    must_fail("icpp_clock_probe null", clk(None, 0.1, None))
+    buf = (ctypes.c_ulonglong * 2)()
+    must_fail("icpp_clock_probe seconds", clk(buf, 100.0, None))
+    rp = fn("icpp_read_probe", i, vp, sz, ctypes.c_uint, i, i, i, i, i, vp, sz, vp)
+    must_fail("icpp_read_probe stripe", rp(P, 1 << 20, 4096, 24, 8, 256, 1, 0, P, 1024, None))
+    must_fail("icpp_read_probe sink", rp(P, 1 << 20, 4096, 128, 8, 256, 1, 0, P, 1, None))
+    if bad:
+        print("\n".join(bad))
+        sys.exit(3)
+    print("ASAN DRIVER OK")
+""")
+
+
+def test_abi_host_code_under_asan():
+    try:
+        from icpp_tuning_amd import build_asan
+    except ImportError:
+        pytest.skip("the host-ASan build tool is not shipped to this machine")
+    if not os.path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc not available")
+    lib = build_asan.build_asan()
+    env = dict(os.environ, LD_PRELOAD=str(build_asan.asan_runtime()),
+               ASAN_OPTIONS="detect_leaks=0:halt_on_error=1:abort_on_error=0:exitcode=41")
+    r = subprocess.run([sys.executable, "-c", DRIVER, str(lib)], env=env, capture_output=True, text=True, timeout=300)
+    out = r.stdout + r.stderr
+    assert "AddressSanitizer" not in out, out[-4000:]
+    assert r.returncode == 0 and "ASAN DRIVER OK" in r.stdout, out[-4000:]
