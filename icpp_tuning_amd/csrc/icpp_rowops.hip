@@ -489,30 +489,33 @@ layernorm_bwd_kernel_long(const T* __restrict__ DY, const T* __restrict__ X, con
 }
 
 // Pass 2 (reference _layer_norm_bwd_dwdb :184-207): dw[n] = sum_g part[g][n],
-// db[n] = sum_g part[g][N + n], summed in a fixed order. Workgroup of 256 = 16
-// columns x 16 partial-row lanes; lane l loads partial rows l, l + 16, ...
-// (G <= 256: at most 16, all issued before the first add), then the 16 lane
-// sums are added in lane order through LDS.
+// db[n] = sum_g part[g][N + n], summed in a fixed order. Workgroup of 256 = 32
+// columns x 8 partial-row lanes, so a wave reads two whole 128-byte row segments
+// per load; lane l sums partial rows l, l + 8, ... (G <= 256: at most 32, all
+// issued before the first add), then the 8 lane sums are added in lane order
+// through LDS.
+constexpr int DWDB_COLS = 32, DWDB_LANES = 8;
 template <typename T>
 __global__ void __launch_bounds__(256)
 layernorm_dwdb_kernel(const float* __restrict__ part, T* __restrict__ DW, T* __restrict__ DB, int G, int N) {
-  __shared__ float acc[16][17];
-  const int col = threadIdx.x & 15, lane_g = threadIdx.x >> 4;
-  const int n2 = blockIdx.x * 16 + col;  // column of the [dw | db] row of length 2N
-  float v[BWD_MAX_GROUPS / 16];
+  __shared__ float acc[DWDB_LANES][DWDB_COLS + 1];
+  const int col = threadIdx.x % DWDB_COLS, lane_g = threadIdx.x / DWDB_COLS;
+  const int n2 = blockIdx.x * DWDB_COLS + col;  // column of the [dw | db] row of length 2N
+  constexpr int PER = BWD_MAX_GROUPS / DWDB_LANES;  // partial rows per lane
+  float v[PER];
 #pragma unroll
-  for (int j = 0; j < BWD_MAX_GROUPS / 16; ++j) {
-    const int g = lane_g + 16 * j;
+  for (int j = 0; j < PER; ++j) {
+    const int g = lane_g + DWDB_LANES * j;
     v[j] = (n2 < 2 * N && g < G) ? part[(size_t)g * 2 * N + n2] : 0.f;
   }
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < BWD_MAX_GROUPS / 16; ++j) s += v[j];
+  for (int j = 0; j < PER; ++j) s += v[j];
   acc[lane_g][col] = s;
   __syncthreads();
   if (lane_g == 0 && n2 < 2 * N) {
     float t = acc[0][col];
-    for (int l = 1; l < 16; ++l) t += acc[l][col];
+    for (int l = 1; l < DWDB_LANES; ++l) t += acc[l][col];
     if (n2 < N) DW[n2] = from_f<T>(t);
     else DB[n2 - N] = from_f<T>(t);
   }
@@ -748,7 +751,8 @@ int ln_bwd_t(const void* DY, const void* X, const void* W, const float* mean, co
     }
   });
   if (e != hipSuccess) return set_error((int)e, hipGetErrorString(e));
-  hipLaunchKernelGGL(layernorm_dwdb_kernel<T>, dim3((2 * N + 15) / 16), dim3(256), 0, s, part, (T*)DW, (T*)DB, G, N);
+  hipLaunchKernelGGL(layernorm_dwdb_kernel<T>, dim3((2 * N + DWDB_COLS - 1) / DWDB_COLS), dim3(256), 0, s, part, (T*)DW,
+                     (T*)DB, G, N);
   e = hipGetLastError();
   return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
 }
