@@ -938,21 +938,32 @@ gemm_kernel(KArgs p) {
         const int n = col0 + wn * G::WTN + cc * CHUNK_ELEMS;
         return n < p.N ? (uint32_t)(r * p.ldc + n) * OSZ : ICPP_OOB_OFFSET;
       };
+      // With few bands every band's residual goes out at once, before the barrier
+      // (one memory latency instead of one per band); otherwise the next band's
+      // loads are in flight while the current band is computed.
+      constexpr bool RES_ALL = HAS_RES && G::TM * NQ <= 8;
       i32x4 rnext[NQ];
+      i32x4 rall[RES_ALL ? G::TM : 1][NQ];
       __amdgpu_buffer_rsrc_t rr_src;
-      auto load_band = [&](int tm) ICPP_INLINE {
+      auto load_band_to = [&](int tm, i32x4 (&dst)[NQ]) ICPP_INLINE {
 #pragma unroll
         for (int j = 0; j < NQ; ++j) {
           const int q = j * 64 + lane;
           // past the range (rows >= M, columns >= N): the hardware returns zeros
-          rnext[j] = ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O)
-                         ? __builtin_amdgcn_raw_buffer_load_b128(rr_src, chunk_off(tm, q), 0, 0)
-                         : i32x4{0, 0, 0, 0};
+          dst[j] = ((MF * CPR_O) % 64 == 0 || q < MF * CPR_O)
+                       ? __builtin_amdgcn_raw_buffer_load_b128(rr_src, chunk_off(tm, q), 0, 0)
+                       : i32x4{0, 0, 0, 0};
         }
       };
+      auto load_band = [&](int tm) ICPP_INLINE { load_band_to(tm, rnext); };
       if constexpr (HAS_RES) {
         rr_src = make_rsrc(res + (size_t)row0 * p.ldc, (uint32_t)(rows * p.ldc * OSZ));
-        load_band(0);
+        if constexpr (RES_ALL) {
+#pragma unroll
+          for (int tm = 0; tm < G::TM; ++tm) load_band_to(tm, rall[tm]);
+        } else {
+          load_band(0);
+        }
       }
       const int w_arr = wave / PER_STAGE;
       char ICPP_LDS* arr = HALO ? (char ICPP_LDS*)halo_lds
@@ -964,9 +975,14 @@ gemm_kernel(KArgs p) {
       for (int tm = 0; tm < G::TM; ++tm) {
         if constexpr (HAS_RES) {
           i32x4 rcur[NQ];
+          if constexpr (RES_ALL) {
 #pragma unroll
-          for (int j = 0; j < NQ; ++j) rcur[j] = rnext[j];
-          if (tm + 1 < G::TM) load_band(tm + 1);
+            for (int j = 0; j < NQ; ++j) rcur[j] = rall[tm][j];
+          } else {
+#pragma unroll
+            for (int j = 0; j < NQ; ++j) rcur[j] = rnext[j];
+            if (tm + 1 < G::TM) load_band(tm + 1);
+          }
 #pragma unroll
           for (int j = 0; j < NQ; ++j) {
             const int q = j * 64 + lane;
