@@ -5,18 +5,18 @@ of efficiency factors (kernel/autotuner/cost_model.py:765-775).  This module
 keeps that contract -- same dataclasses, same builder functions, same factor
 functions, same ``score_formula`` -- so that descriptors written for the
 reference work unchanged, and so the published A100 scores can be reproduced
-(reference mode).  On a spec that carries an MFMA model (MI355X) the same
-factors are evaluated with CDNA4 quantities and one extra factor is applied:
+(reference mode, ``GPUSpec.has_mfma_model == False``: every formula below
+reduces exactly to the reference's).
 
-* threads = waves x 64, LDS bytes use each operand's element size (fp8 = 1),
-  VGPR pressure comes from the MFMA accumulator layout (``vgpr_estimate``),
-  residency is limited per SIMD (8 waves, 512 registers per lane),
-* ``eff_mfma``: MFMA shape issue rate (32x32 shapes sustain a higher rate than
-  16x16 ones on gfx950), LDS read bandwidth per MFMA cycle, and L2 feed rate
-  per CU for small tiles.
-
-Reference mode is selected by ``GPUSpec.has_mfma_model == False``; every
-formula below reduces exactly to the reference's in that mode.
+On a spec that carries an MFMA model (MI355X) ``score_formula`` is instead
+the predicted fraction of dense MFMA peak of one launch, from a per-CU
+schedule model (``predict_schedule``): rounds of co-resident workgroups, per
+K step the largest of MFMA issue, LDS traffic and L2 feed, or the memory
+latency over the prefetch depth; the epilogue's stores and FLOPs; the HBM
+floor; and the split-K reduction launch.  Threads are waves x 64, LDS bytes
+use each operand's element size (fp8 = 1), residency is limited per SIMD (8
+waves, 512 registers per lane) with the compiler's register counts.  The
+descriptors' split-K adjustments of the reference are part of that model.
 """
 
 from __future__ import annotations
@@ -351,31 +351,39 @@ class ModelConstants:
     conv_preferred_block_m: Tuple[float, float] = (32.0, 64.0)
     conv_preferred_block_n: Tuple[float, float] = (64.0, 128.0)
     conv_block_k_free: int = 32
-    # CDNA4-only terms (unused in reference mode)
+    # CDNA4 schedule model (unused in reference mode)
     mfma_rate: Tuple[Tuple[str, float], ...] = ()
     l2_bytes_per_clk_per_cu: float = 0.0
-    lds_exponent: float = 0.5
-    l2_exponent: float = 0.5
+    mem_latency_clk: float = 0.0
+    step_overhead_clk: float = 0.0
+    tile_overhead_clk: float = 0.0
+    store_bytes_per_clk_per_cu: float = 0.0
+    epilogue_flops_per_clk_per_cu: float = 0.0
+    hbm_efficiency: float = 1.0
+    reduce_efficiency: float = 1.0
+    launch_overhead_s: float = 0.0
 
 
 REFERENCE_CONSTANTS = ModelConstants()
 
-# CDNA4: MFMA kernels hide latency with register tiles, not with many resident
-# waves, so the preferred occupancy is one wave per SIMD (4 of 32 slots) and the
-# preferred outputs per lane are those of a 128x128-per-wave tile range.  The
-# MFMA rates are relative sustained issue rates measured on MI355X with a
-# dependency-free MFMA stream (32x32x16 bf16: 1970 TFLOP/s, 16x16x32 bf16:
-# 1711 TFLOP/s; fp8 16x16x128: 4579 TFLOP/s).
+# CDNA4 schedule-model constants.  The MFMA rates are relative sustained issue
+# rates measured on MI355X with a dependency-free MFMA stream (32x32x16 bf16:
+# 1970 TFLOP/s, 16x16x32 bf16: 1711 TFLOP/s; fp8 16x16x128: 4579 TFLOP/s).  The
+# other values are effective rates and latencies fitted to the shipped offline
+# databases (every compiled config timed at every profiled shape): they are
+# what ranks the compiled configs best on those shapes, checked on shapes the
+# fit never saw, not independent hardware measurements.
 CDNA4_CONSTANTS = ModelConstants(
-    preferred_occupancy=0.125,
-    high_warp_free_count=8,
-    mainloop_target_outputs_per_thread=128.0,
-    mainloop_min_outputs_per_thread=16.0,
-    conv_preferred_block_m=(64.0, 128.0),
-    conv_preferred_block_n=(64.0, 128.0),
-    conv_block_k_free=64,
     mfma_rate=(("16x16x32", 0.87), ("32x32x16", 1.0), ("16x16x128", 1.0), ("32x32x64", 1.0)),
-    l2_bytes_per_clk_per_cu=64.0,
+    l2_bytes_per_clk_per_cu=22.5,
+    mem_latency_clk=2400.0,
+    step_overhead_clk=7.5,
+    tile_overhead_clk=3000.0,
+    store_bytes_per_clk_per_cu=4.75,
+    epilogue_flops_per_clk_per_cu=256.0,
+    hbm_efficiency=0.81,
+    reduce_efficiency=0.7,
+    launch_overhead_s=0.6e-6,
 )
 
 
@@ -417,14 +425,8 @@ def _estimate_occupancy(config: TuneConfig, hw: GPUSpec) -> float:
     return min(1.0, _resident_blocks_per_sm(config, hw) * config.num_warps / hw.max_warps_per_sm)
 
 
-def _preferred_block_k(op: OpSpec, hw: Optional[GPUSpec] = None) -> int:
+def _preferred_block_k(op: OpSpec) -> int:
     K = op.K
-    if hw is not None and hw.has_mfma_model:
-        # one 16x16 MFMA step is 64 bytes of K per lane group; two steps per tile
-        pref = 128 // op.mainloop.input_element_bytes
-        while pref > 16 and K < pref:
-            pref //= 2
-        return pref
     if K >= 64:
         return 64
     if K >= 32:
@@ -454,15 +456,9 @@ def _estimate_operand_reuse(op: OpSpec, config: TuneConfig, tiles_M: int) -> Tup
 
 
 def _preferred_num_stages(op: OpSpec, config: TuneConfig, tile_ai: float, hw: GPUSpec) -> int:
-    ridge = hw.ridge_point(op.mainloop.dtype) if hw.has_mfma_model else hw.ridge_point_fp16
+    ridge = hw.ridge_point_fp16
     mem_eff = 1.0 if ridge <= 0 else min(1.0, tile_ai / ridge)
     k_iters = max(1, _ceildiv(op.K, config.block_K))
-    if hw.has_mfma_model:
-        # The gfx950 templates hold one tile in LDS while the next one is in
-        # flight in registers: 2 LDS stages cover HBM latency when the tile is
-        # compute-bound; memory-bound tiles ask for a deeper pipeline.
-        pref = 2 + (1 if mem_eff < 0.5 else 0)
-        return min(max(1, pref), max(1, min(4, k_iters)))
     pref = 2
     if op.mainloop.kind == "implicit_gemm_conv":
         pref += 1
@@ -537,14 +533,14 @@ def eff_mainloop(op: OpSpec, config: TuneConfig, proj: ConfigProjection,
     target = c.mainloop_min_outputs_per_thread + (
         c.mainloop_target_outputs_per_thread - c.mainloop_min_outputs_per_thread) * signal
     thread_eff = 1.0 / (1.0 + c.mainloop_output_distance_penalty * _log2_distance(proj.outputs_per_thread, target))
-    k_eff = math.sqrt(min(1.0, config.block_K / _preferred_block_k(op, hw)))
+    k_eff = math.sqrt(min(1.0, config.block_K / _preferred_block_k(op)))
     return padding_eff * thread_eff * k_eff
 
 
 def eff_memory(op: OpSpec, config: TuneConfig, proj: ConfigProjection, hw: GPUSpec) -> float:
     """Tile arithmetic intensity against the roofline ridge, x LDS footprint."""
     c = constants_for(hw)
-    ridge = hw.ridge_point(op.mainloop.dtype) if hw.has_mfma_model else hw.ridge_point_fp16
+    ridge = hw.ridge_point_fp16
     if ridge <= 0:
         return 1.0
     roof = min(1.0, proj.tile_arithmetic_intensity / ridge)
@@ -612,7 +608,7 @@ def eff_implicit_conv(op: OpSpec, config: TuneConfig, proj: ConfigProjection, hw
         warp_eff = 1.0
     stage_eff = 1.0
     if config.num_stages > 1:
-        ridge = hw.ridge_point(op.mainloop.dtype) if hw.has_mfma_model else hw.ridge_point_fp16
+        ridge = hw.ridge_point_fp16
         pressure = 1.0 - min(1.0, proj.tile_arithmetic_intensity / ridge) if ridge > 0 else 0.0
         stage_eff = 1.0 / (1.0 + 0.25 * (config.num_stages - 1) * sig * pressure)
     return m_eff * n_eff * warp_eff * stage_eff * base
@@ -663,36 +659,106 @@ def eff_reduction(op: OpSpec, config: TuneConfig, proj: ConfigProjection,
     return prod ** (1.0 / len(reds))
 
 
-def eff_mfma(op: OpSpec, config: TuneConfig, proj: ConfigProjection, hw: GPUSpec) -> float:
-    """CDNA4 matrix-core feed: MFMA shape rate x LDS read bandwidth x L2 feed.
+# ---------------------------------------------------------------------------
+# CDNA4 schedule model
+# ---------------------------------------------------------------------------
 
-    Per K tile, each wave reads its A rows and B columns from LDS once
-    ((WTM + WTN) * BK * bytes) and issues (WTM/mf)(WTN/mf)(BK/kf) MFMAs.  The
-    waves of a workgroup spread over the 4 SIMDs, so LDS time per K tile is
-    total bytes / lds_bytes_per_clk and MFMA time is per-SIMD issue cycles.
-    The L2 term compares the tile's global bytes per MFMA cycle with what one
-    CU can pull from L2.  Returns 1 in reference mode.
+
+def _operand_bytes(op: OpSpec, split_k: int) -> float:
+    """A and B bytes of the whole launch (a split-K spec carries K / split_k)."""
+    m = op.mainloop
+    if m.kind == "gemm":
+        k = m.K * split_k
+        return float(m.M * k * m.input_element_bytes + k * m.N * m.weight_element_bytes)
+    return float(m.input_elements * m.input_element_bytes + m.weight_elements * m.weight_element_bytes)
+
+
+def ideal_seconds(op: OpSpec, config: TuneConfig, hw: GPUSpec) -> float:
+    """Mainloop FLOPs of the whole launch at the dtype's dense MFMA peak."""
+    flops = op.mainloop.flops_per_fma * op.M * op.N * op.K * max(1, config.split_k)
+    return flops / (hw.peak_tflops(op.mainloop.dtype) * 1e12)
+
+
+def predict_schedule(op: OpSpec, config: TuneConfig, hw: GPUSpec,
+                     c: Optional[ModelConstants] = None) -> Dict[str, float]:
+    """Predicted time of one launch on a CDNA4 device, in seconds.
+
+    Workgroups are spread evenly over the CUs: the busiest CU runs
+    ``n_cu = ceil(grid / CUs)`` tiles, ``conc`` of them at once (residency
+    from registers, LDS and wave slots), in ``rounds = ceil(n_cu / conc)``.
+    One K step of one workgroup needs
+
+      MFMA   (BM/m)(BN/n)(BK/k) issue cycles / sustained rate, spread over
+             min(4, waves on the CU) SIMDs,
+      LDS    every wave reads its A rows and B columns, and the tile is
+             written once: (waves (WTM + WTN) + BM + BN) BK bytes at
+             ``hw.lds_bytes_per_clk``,
+      L2     (BM + BN) BK bytes at the per-CU L2 feed rate.
+
+    The mainloop is the larger of the throughput bound (all n_cu tiles share
+    the CU's SIMDs, LDS and L2 port) and the latency bound (each round walks
+    its K steps one after another; a step cannot beat the memory latency
+    divided by the prefetch depth ``num_stages - 1``, plus a fixed per-step
+    cost).  Each round then stores its tiles (fp32 partials under split-K)
+    and runs the epilogue primitives' FLOPs, plus a fixed per-tile cost.  The
+    launch cannot beat its operands and outputs at HBM rate; split-K adds the
+    reduction launch (read every partial, write the output).
     """
-    if not hw.has_mfma_model:
-        return 1.0
-    c = constants_for(hw)
-    rate = dict(c.mfma_rate).get(config.mfma, 1.0) if config.mfma else 1.0
+    c = c or constants_for(hw)
+    proj = project_config(op, config, hw)
+    sk = max(1, config.split_k)
+    waves = max(1, config.num_warps)
+    simds = max(1, hw.simds_per_cu)
+    clk = hw.clock_ghz * 1e9
+    n_cu = _ceildiv(proj.grid_size, hw.num_sm)
+    conc = max(1, min(proj.resident_blocks_per_sm, n_cu))
+    rounds = _ceildiv(n_cu, conc)
+
     shape = hw.mfma(op.mainloop.dtype, config.mfma) if config.mfma else None
-    if shape is None:
-        return rate
+    if shape is not None:
+        rate = dict(c.mfma_rate).get(config.mfma, 1.0)
+        issue = (max(1, config.block_M // shape.m) * max(1, config.block_N // shape.n)
+                 * max(1, config.block_K // shape.k) * shape.cycles / rate)
+    else:   # no MFMA shape: the dtype's dense peak per SIMD
+        per_simd = hw.peak_tflops(op.mainloop.dtype) * 1e12 / (hw.num_sm * simds * clk)
+        issue = op.mainloop.flops_per_fma * config.block_M * config.block_N * config.block_K / per_simd
+    # waves sit on SIMDs round-robin: the busiest SIMD holds ceil(waves / 4)
+    mfma_shared = _ceildiv(conc * waves, simds) * issue / (waves * conc)
+    mfma_alone = _ceildiv(waves, simds) * issue / waves
     wm, wn = config.wave_grid()
-    wtm, wtn = config.block_M // wm, config.block_N // wn
-    mfmas_per_wave = max(1, wtm // shape.m) * max(1, wtn // shape.n) * max(1, config.block_K // shape.k)
-    waves_per_simd = max(1.0, config.num_warps / hw.simds_per_cu)
-    mfma_cycles = mfmas_per_wave * shape.cycles * waves_per_simd
-    esz = config.a_bytes
-    lds_bytes = config.num_warps * (wtm + wtn) * config.block_K * esz
-    lds_cycles = lds_bytes / max(1, hw.lds_bytes_per_clk)
-    lds_eff = min(1.0, mfma_cycles / max(1e-9, lds_cycles)) ** c.lds_exponent
-    gl_bytes = (config.block_M + config.block_N) * config.block_K * esz
-    l2_cycles = gl_bytes / max(1e-9, c.l2_bytes_per_clk_per_cu)
-    l2_eff = min(1.0, mfma_cycles / max(1e-9, l2_cycles)) ** c.l2_exponent
-    return rate * lds_eff * l2_eff
+    wtm, wtn = config.block_M // max(1, wm), config.block_N // max(1, wn)
+    ab, bb = op.mainloop.input_element_bytes, op.mainloop.weight_element_bytes
+    steps = proj.tiles_K
+    step_bytes = (config.block_M * ab + config.block_N * bb) * config.block_K
+    lds = (waves * (wtm * ab + wtn * bb) * config.block_K + step_bytes) / max(1, hw.lds_bytes_per_clk)
+    l2 = step_bytes / c.l2_bytes_per_clk_per_cu
+    latency = c.mem_latency_clk / max(1, config.num_stages - 1)
+    t_thru = n_cu * steps * max(mfma_shared, lds, l2)
+    t_lat = rounds * steps * (max(mfma_alone, lds, l2, latency) + c.step_overhead_clk)
+    mainloop_clk = max(t_thru, t_lat)
+
+    outs = proj.tile_outputs
+    out_b = 4 if sk > 1 else op.mainloop.output_element_bytes
+    store = outs * (out_b + sum(p.bytes_per_output for p in op.epilogue)) / c.store_bytes_per_clk_per_cu
+    epi = outs * sum(p.flops_per_output for p in op.epilogue) / c.epilogue_flops_per_clk_per_cu
+    epilogue_clk = rounds * (store + epi + c.tile_overhead_clk)
+
+    bw = hw.mem_bandwidth_gbps * 1e9 * c.hbm_efficiency
+    mn = float(op.M * op.N)
+    hbm_s = (_operand_bytes(op, sk) + mn * out_b * sk
+             + mn * sum(p.bytes_per_output for p in op.epilogue)) / bw
+    kernel_s = max((mainloop_clk + epilogue_clk) / clk, hbm_s)
+    reduce_s = ((mn * 4 * sk + mn * op.mainloop.output_element_bytes) / (bw * c.reduce_efficiency)
+                + c.launch_overhead_s if sk > 1 else 0.0)
+    return {"seconds": kernel_s + reduce_s, "kernel_s": kernel_s, "reduce_s": reduce_s, "hbm_s": hbm_s,
+            "mainloop_s": mainloop_clk / clk, "epilogue_s": epilogue_clk / clk,
+            "throughput_bound": t_thru >= t_lat, "n_cu": n_cu, "concurrent": conc, "rounds": rounds}
+
+
+def extra_pass_seconds(op: OpSpec, hw: GPUSpec, bytes_moved: float) -> float:
+    """A separate memory-bound launch (e.g. a normalisation pass over the output)."""
+    c = constants_for(hw)
+    return bytes_moved / (hw.mem_bandwidth_gbps * 1e9 * c.hbm_efficiency) + c.launch_overhead_s
 
 
 # ---------------------------------------------------------------------------
@@ -710,27 +776,36 @@ def _factors(op: OpSpec, config: TuneConfig, hw: GPUSpec):
         "eff_implicit_conv": eff_implicit_conv(op, config, proj, hw),
         "eff_epilogue": eff_epilogue(op, config, proj, hw),
         "eff_reduction": eff_reduction(op, config, proj, hw),
-        "eff_mfma": eff_mfma(op, config, proj, hw),
     }
     return proj, f
 
 
 def score_formula(op: OpSpec, config: TuneConfig, hw: GPUSpec) -> float:
+    """Reference mode: the product of the seven factors.  CDNA4 mode: the
+    predicted fraction of dense MFMA peak, ideal_seconds / predicted seconds."""
+    if hw.has_mfma_model:
+        return ideal_seconds(op, config, hw) / predict_schedule(op, config, hw)["seconds"]
     _, f = _factors(op, config, hw)
     s = 1.0
     for name in ("eff_mainloop", "eff_memory", "eff_parallel", "eff_pipeline",
-                 "eff_implicit_conv", "eff_epilogue", "eff_reduction", "eff_mfma"):
+                 "eff_implicit_conv", "eff_epilogue", "eff_reduction"):
         s *= f[name]
     return s
 
 
 def score_formula_detailed(op: OpSpec, config: TuneConfig, hw: GPUSpec) -> dict:
-    proj, f = _factors(op, config, hw)
-    score = 1.0
-    for v in f.values():
-        score *= v
-    out = {"score": score}
-    out.update(f)
+    if hw.has_mfma_model:
+        sched = predict_schedule(op, config, hw)
+        ideal = ideal_seconds(op, config, hw)
+        out = {"score": ideal / sched["seconds"], "ideal_s": ideal, "schedule": sched}
+        proj = project_config(op, config, hw)
+    else:
+        proj, f = _factors(op, config, hw)
+        score = 1.0
+        for v in f.values():
+            score *= v
+        out = {"score": score}
+        out.update(f)
     out["projection"] = {k: getattr(proj, k) for k in (
         "tiles_M", "tiles_N", "tiles_K", "grid_size", "tile_outputs", "outputs_per_thread",
         "mainloop_iterations", "tile_arithmetic_intensity", "occupancy", "resident_blocks_per_sm",
@@ -754,7 +829,8 @@ __all__ = [
     "ACT_PRIMITIVE", "BATCHNORM", "BIAS_ADD", "CDNA4_CONSTANTS", "ConfigProjection", "FusionPrimitive",
     "GELU", "MainloopSpec", "ModelConstants", "OpSpec", "PRIMITIVE_LIBRARY", "REFERENCE_CONSTANTS",
     "RELU", "ROW_LAYERNORM", "SILU", "TuneConfig", "conv_output_hw", "constants_for", "eff_epilogue",
-    "eff_implicit_conv", "eff_mainloop", "eff_memory", "eff_mfma", "eff_parallel", "eff_pipeline",
-    "eff_reduction", "make_conv2d_spec", "make_matmul_spec", "project_config", "resolve_primitives",
+    "eff_implicit_conv", "eff_mainloop", "eff_memory", "eff_parallel", "eff_pipeline",
+    "eff_reduction", "extra_pass_seconds", "ideal_seconds", "make_conv2d_spec", "make_matmul_spec",
+    "predict_schedule", "project_config", "resolve_primitives",
     "score_configs", "score_formula", "score_formula_detailed", "select_best_config",
 ]

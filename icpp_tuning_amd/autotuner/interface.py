@@ -22,7 +22,7 @@ from dataclasses import dataclass, field
 from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple, Union
 
 from .._lib import IcppCallError
-from .cost_model import OpSpec, TuneConfig, score_formula, score_formula_detailed
+from .cost_model import OpSpec, TuneConfig, ideal_seconds, score_formula, score_formula_detailed
 from .gpu_spec import GPUSpec, get_gpu_spec
 
 
@@ -56,6 +56,12 @@ class TileLangKernelBase:
     def schedule_factor(self, raw: Dict[str, Any]) -> float:
         """Relative mainloop efficiency of the config's schedule (1 for the default one)."""
         return 1.0
+
+    def extra_seconds(self, raw: Dict[str, Any], hw: GPUSpec, **shape_kwargs: Any) -> float:
+        """Time of launches the config adds beside the scored kernel (e.g. a
+        separate normalisation pass over the output).  Used by the CDNA4
+        schedule model only, whose score is a time ratio; 0 by default."""
+        return 0.0
 
     def format_config(self, raw: Dict[str, Any]) -> str:
         """``BM{}_BN{}_BK{}[_SK{}]_S{}_T{}`` (reference :117-128), plus the MFMA
@@ -96,6 +102,13 @@ def _score(descriptor: TileLangKernelBase, raw, hw, detailed: bool, shape):
         base = detail["score"]
     else:
         base, detail = score_formula(op, cfg, hw), None
+    if hw.has_mfma_model:
+        extra = descriptor.extra_seconds(raw, hw, **shape)
+        if extra > 0.0 and base > 0.0:
+            ideal = ideal_seconds(op, cfg, hw)
+            base = ideal / (ideal / base + extra)
+        if detail is not None:
+            detail["extra_s"] = extra
     return descriptor.score_adjustment(raw, base * descriptor.schedule_factor(raw), **shape), detail
 
 

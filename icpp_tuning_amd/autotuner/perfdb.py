@@ -334,7 +334,25 @@ def evaluate(descriptor: TileLangKernelBase, db: Optional[PerformanceDB], shapes
             log(f"[perfdb-eval] {descriptor.name} {shape}: oracle {row['oracle']} {res.best_ms * 1e3:.1f} us, "
                 f"{sel.level} {pick} {(row['pick_ms'] or float('nan')) * 1e3:.1f} us, formula {formula} "
                 f"{row['formula_ms'] * 1e3:.1f} us")
+    return _report(descriptor, rows)
 
+
+def rescore(descriptor: TileLangKernelBase, report: Dict[str, Any], hw: Optional[GPUSpec] = None) -> Dict[str, Any]:
+    """Re-pick the formula's top-1 of every row of an `evaluate` report with the
+    current cost model and score it against the times the row already holds
+    (every compiled config was measured there): no device work."""
+    hw = hw or get_gpu_spec()
+    rows = []
+    for r in report["rows"]:
+        formula = descriptor.format_config(select_best(descriptor, hw, **r["shape"])[0])
+        row = dict(r, formula=formula, formula_ms=r["ms"][formula])
+        if r["level"] == "formula":      # a table miss falls back to the formula's pick
+            row.update(pick=formula, pick_ms=r["ms"][formula])
+        rows.append(row)
+    return _report(descriptor, rows)
+
+
+def _report(descriptor: TileLangKernelBase, rows: List[Dict[str, Any]]) -> Dict[str, Any]:
     def summary(key, sel_rows):
         sel_rows = [r for r in sel_rows if r[key + "_ms"] is not None]
         if not sel_rows:
@@ -413,9 +431,17 @@ def main(argv=None) -> int:  # pragma: no cover - device tool
     ap.add_argument("--budget-ms", type=float, default=0.0)
     ap.add_argument("--eval-out", default="", help="also evaluate on held-out shapes and write the report here")
     ap.add_argument("--eval-only", action="store_true", help="evaluate the database at --out (or the shipped one)")
+    ap.add_argument("--rescore", default="", help="an --eval-out report: re-pick its formula column with the "
+                    "current cost model against the times it holds (no device work), write to --eval-out")
     a = ap.parse_args(argv)
     desc = ops[a.op]
     hw = get_gpu_spec()
+    if a.rescore:
+        rep = rescore(desc, json.loads(Path(a.rescore).read_text()), hw)
+        if a.eval_out:
+            Path(a.eval_out).write_text(json.dumps(rep, indent=1))
+        print(json.dumps({k: rep[k] for k in ("op", "table", "formula", "combined", "pruned_set")}), flush=True)
+        return 0
     shapes = default_plan(a.op, hw)
     out = Path(a.out) if a.out else shipped_path(op_key(desc), hw)
     if a.eval_only:

@@ -9,7 +9,8 @@ exactly one compiled instance of libicpp_hip.so (plus a split-K factor), so
 
 from __future__ import annotations
 
-from typing import Any, Dict, List, Optional, Sequence
+import functools
+from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 from ..autotuner.cost_model import TuneConfig
 from ..autotuner.gpu_spec import GPUSpec
@@ -18,9 +19,10 @@ from ..autotuner.search_space import prune_for_shape
 from ..instances import ESZ, FAMILY_ID, INSTANCES, MFMA_K, Inst
 
 
-def family_instances(family: str) -> List[Inst]:
+@functools.lru_cache(maxsize=None)
+def family_instances(family: str) -> Tuple[Inst, ...]:
     """Instances of a family in library index order (the ABI sorts by name)."""
-    return sorted((i for i in INSTANCES if i.family == family), key=lambda i: i.name)
+    return tuple(sorted((i for i in INSTANCES if i.family == family), key=lambda i: i.name))
 
 
 def raw_from_inst(inst: Inst, split_k: Optional[int] = None) -> Dict[str, Any]:

@@ -54,18 +54,6 @@ class Conv2dDescriptor(InstanceDescriptor):
         OH, OW = calc_oh_ow(H, W, KH, KW, stride, padding, 1)
         return N * OH * OW, OC
 
-    def score_adjustment(self, raw, base_score, **shape):
-        sk = raw.get("split_k", 1)
-        if sk <= 1:
-            return base_score
-        from ..autotuner.gpu_spec import get_gpu_spec
-        hw = get_gpu_spec()
-        M, F = self.gemm_mn(**shape)
-        K = self.k_extent(**shape)
-        t_main = 2.0 * M * F * K / (hw.peak_tflops("f16") * 1e12)
-        t_red = (2.0 * sk * M * F * 4 + M * F * 2) / (hw.mem_bandwidth_gbps * 1e9) + 4e-6
-        return base_score * t_main / (t_main + t_red)
-
     def flops(self, N=0, C=0, H=0, W=0, OC=0, KH=3, KW=3, stride=1, padding=0, **kw):
         OH, OW = calc_oh_ow(H, W, KH, KW, stride, padding, 1)
         return float(calc_conv_flops(N, C, OH, OW, OC, KH, KW))

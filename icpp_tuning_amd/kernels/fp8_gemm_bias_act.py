@@ -12,7 +12,6 @@ from __future__ import annotations
 import torch
 
 from ..autotuner.cost_model import ACT_PRIMITIVE, make_matmul_spec
-from ..autotuner.gpu_spec import get_gpu_spec
 from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from ._base import InstanceDescriptor
@@ -36,16 +35,6 @@ class Fp8GemmBiasActDescriptor(InstanceDescriptor):
         sk = raw_config.get("split_k", 1) if raw_config else 1
         return make_matmul_spec(M=M, N=N, K=K // sk, primitives=["bias_add", ACT_PRIMITIVE[self.act]],
                                 dtype="fp8", output_element_bytes=2)
-
-    def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
-        sk = raw.get("split_k", 1)
-        if sk <= 1:
-            return base_score
-        hw = get_gpu_spec()
-        t_main = max(2.0 * M * N * K / (hw.peak_tflops("fp8") * 1e12),
-                     (M * K + K * N) / (hw.mem_bandwidth_gbps * 1e9))
-        t_red = (2.0 * sk * M * N * 4 + M * N * 2) / (hw.mem_bandwidth_gbps * 1e9) + 4e-6
-        return base_score * t_main / (t_main + t_red)
 
     def make_inputs(self, M, N, K, **kw):
         d = _inputs.config5(M, N, K, device="cuda")

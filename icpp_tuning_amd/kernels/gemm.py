@@ -9,13 +9,11 @@ the reference's ``T.atomic_add`` into an uninitialised output (gemm.py:78).
 
 from __future__ import annotations
 
-import math
 from typing import Any, Dict, Optional
 
 import torch
 
 from ..autotuner.cost_model import make_matmul_spec
-from ..autotuner.gpu_spec import get_gpu_spec
 from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from .. import runtime
@@ -35,18 +33,6 @@ class GemmDescriptor(InstanceDescriptor):
         sk = raw_config.get("split_k", 1) if raw_config else 1
         return make_matmul_spec(M=M, N=N, K=K // sk, dtype=self.dtype)
 
-    def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
-        """Split-K pays an fp32 partial write + read per split and a reduction
-        launch: scale by t_mainloop / (t_mainloop + t_reduce) at roofline rates."""
-        sk = raw.get("split_k", 1)
-        if sk <= 1:
-            return base_score
-        hw = get_gpu_spec()
-        t_main = 2.0 * M * N * K / (hw.peak_tflops(self.dtype) * 1e12)
-        t_red = (2.0 * sk * M * N * 4 + M * N * 2) / (hw.mem_bandwidth_gbps * 1e9) + 4e-6
-        return base_score * t_main / (t_main + t_red)
-
-    # ---- tune() hooks ------------------------------------------------------
     def make_inputs(self, M, N, K, **kw):
         d = _inputs.config1(M, N, K, device="cuda")
         d["C"] = torch.empty((M, N), dtype=torch.float16, device="cuda")

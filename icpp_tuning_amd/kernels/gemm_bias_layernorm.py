@@ -24,7 +24,7 @@ from typing import Any, Dict, List, Optional
 
 import torch
 
-from ..autotuner.cost_model import make_matmul_spec
+from ..autotuner.cost_model import extra_pass_seconds, make_matmul_spec
 from ..autotuner.perfdb import select_config
 from .. import inputs as _inputs
 from .. import runtime
@@ -42,6 +42,11 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
         return "gemm_bias_layernorm"
 
     def make_op_spec(self, raw_config=None, M=0, N=0, K=0, **kw):
+        """The GEMM launch of the strategy: "gemm_ln" is a plain GEMM + bias (the
+        LayerNorm runs in a pass of its own); the other two carry the row
+        statistics in their epilogue."""
+        if raw_config is not None and raw_config.get("strategy") == "gemm_ln":
+            return make_matmul_spec(M=M, N=N, K=K, primitives=["bias_add"], dtype=self.dtype)
         return make_matmul_spec(M=M, N=N, K=K, primitives=["bias_add", "row_layernorm"], dtype=self.dtype)
 
     def _family(self, raw) -> str:
@@ -79,15 +84,12 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
     def format_config(self, raw):
         return super().format_config(raw) + {"row": "_ROW", "gemm_ln": "_GL"}.get(raw.get("strategy"), "_2P")
 
-    def score_adjustment(self, raw, base_score, M=0, N=0, K=0, **kw):
-        """Two-pass and GEMM-then-LN pay one extra read + write of Y at HBM rate (roofline ratio)."""
+    def extra_seconds(self, raw, hw, M=0, N=0, K=0, **kw):
+        """Two-pass and GEMM-then-LN run a second launch that reads and writes Y."""
         if raw.get("strategy") == "row":
-            return base_score
-        from ..autotuner.gpu_spec import get_gpu_spec
-        hw = get_gpu_spec()
-        t_main = 2.0 * M * N * K / (hw.peak_tflops("f16") * 1e12)
-        t_fin = (2.0 * M * N * 2) / (hw.mem_bandwidth_gbps * 1e9) + 3e-6
-        return base_score * t_main / (t_main + t_fin)
+            return 0.0
+        op = self.make_op_spec(raw, M=M, N=N, K=K)
+        return extra_pass_seconds(op, hw, 2.0 * M * N * op.mainloop.output_element_bytes)
 
     def make_inputs(self, M, N, K, **kw):
         d = _inputs.config3(M, N, K, device="cuda")
