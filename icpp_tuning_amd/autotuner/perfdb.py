@@ -34,7 +34,7 @@ from pathlib import Path
 from typing import Any, Dict, Iterable, List, Optional, Sequence, Tuple
 
 from .gpu_spec import GPUSpec, get_gpu_spec
-from .interface import TileLangKernelBase, select_best, tune
+from .interface import TileLangKernelBase, rank_all, select_best, tune
 
 SHIPPED_DIR = Path(__file__).resolve().parents[1] / "perf_db"
 
@@ -323,11 +323,13 @@ def evaluate(descriptor: TileLangKernelBase, db: Optional[PerformanceDB], shapes
         ms = {descriptor.format_config(c["config"]): c["ms"] for c in res.candidates}
         kept = {descriptor.format_config(c) for c in descriptor.prune(descriptor.get_raw_configs(**shape), hw, **shape)}
         sel = tuner.select(**shape)
-        formula = descriptor.format_config(select_best(descriptor, hw, **shape)[0])
+        ranked = _formula_ranking(descriptor, hw, shape)
+        formula = ranked[0]
         pick = descriptor.format_config(sel.config)
         row = {"shape": dict(shape), "oracle": descriptor.format_config(res.best_config), "oracle_ms": res.best_ms,
                "level": sel.level, "pick": pick, "pick_ms": ms.get(pick), "formula": formula,
-               "formula_ms": ms[formula], "pruned_best_ms": min(v for k, v in ms.items() if k in kept),
+               "formula_ms": ms[formula], "formula_ranking": ranked,
+               "pruned_best_ms": min(v for k, v in ms.items() if k in kept),
                "n_measured": len(ms), "n_pruned_set": len(kept), "ms": ms}
         rows.append(row)
         if log:
@@ -344,15 +346,33 @@ def rescore(descriptor: TileLangKernelBase, report: Dict[str, Any], hw: Optional
     hw = hw or get_gpu_spec()
     rows = []
     for r in report["rows"]:
-        formula = descriptor.format_config(select_best(descriptor, hw, **r["shape"])[0])
-        row = dict(r, formula=formula, formula_ms=r["ms"][formula])
+        ranked = _formula_ranking(descriptor, hw, r["shape"])
+        formula = ranked[0]
+        row = dict(r, formula=formula, formula_ms=r["ms"][formula], formula_ranking=ranked)
         if r["level"] == "formula":      # a table miss falls back to the formula's pick
             row.update(pick=formula, pick_ms=r["ms"][formula])
         rows.append(row)
     return _report(descriptor, rows)
 
 
+TOPK = (1, 2, 4, 8)
+
+
+def _formula_ranking(descriptor: TileLangKernelBase, hw: GPUSpec, shape: Dict[str, Any]) -> List[str]:
+    """The formula's first max(TOPK) configs for the shape (pruned, best first;
+    the first is `select_best`'s pick)."""
+    return [e["formatted"] for e in rank_all(descriptor, hw, **shape)[:max(TOPK)]]
+
+
 def _report(descriptor: TileLangKernelBase, rows: List[Dict[str, Any]]) -> Dict[str, Any]:
+    def topk(k):
+        """A measured search of the formula's top k (tune() without seeds, top_k=k):
+        the fastest of those k against the oracle."""
+        ratios = [r["oracle_ms"] / min(r["ms"][c] for c in r["formula_ranking"][:k])
+                  for r in rows if r.get("formula_ranking")]
+        return {"n": len(ratios), "perf_ratio_mean": sum(ratios) / max(1, len(ratios)),
+                "perf_ratio_min": min(ratios, default=0.0)}
+
     def summary(key, sel_rows):
         sel_rows = [r for r in sel_rows if r[key + "_ms"] is not None]
         if not sel_rows:
@@ -364,7 +384,8 @@ def _report(descriptor: TileLangKernelBase, rows: List[Dict[str, Any]]) -> Dict[
     table_rows = [r for r in rows if r["level"] == "table"]
     pr = [r["oracle_ms"] / r["pruned_best_ms"] for r in rows]
     return {"op": op_key(descriptor), "rows": rows, "table": summary("pick", table_rows),
-            "formula": summary("formula", rows), "combined": summary("pick", rows),
+            "formula": summary("formula", rows), "formula_topk": {str(k): topk(k) for k in TOPK},
+            "combined": summary("pick", rows),
             "pruned_set": {"n": len(rows), "perf_ratio_mean": sum(pr) / max(1, len(pr)), "perf_ratio_min": min(pr, default=0)}}
 
 
@@ -440,7 +461,8 @@ def main(argv=None) -> int:  # pragma: no cover - device tool
         rep = rescore(desc, json.loads(Path(a.rescore).read_text()), hw)
         if a.eval_out:
             Path(a.eval_out).write_text(json.dumps(rep, indent=1))
-        print(json.dumps({k: rep[k] for k in ("op", "table", "formula", "combined", "pruned_set")}), flush=True)
+        print(json.dumps({k: rep[k] for k in ("op", "table", "formula", "formula_topk", "combined", "pruned_set")}),
+              flush=True)
         return 0
     shapes = default_plan(a.op, hw)
     out = Path(a.out) if a.out else shipped_path(op_key(desc), hw)

@@ -73,3 +73,22 @@ def test_layernorm_second_pass_is_priced():
         if strategy == "gemm_ln":      # a plain GEMM + bias launch: no statistics epilogue
             assert [p.name for p in desc.make_op_spec(e["raw_config"], M=M, N=N, K=K).epilogue] == ["bias_add"]
     assert seen == {"row", "two_pass", "gemm_ln"}
+
+
+def test_report_topk_is_the_best_measured_of_the_ranking():
+    """`formula_topk[k]`: the fastest measured config among the formula's first k
+    against the oracle, i.e. what tune(top_k=k) without seeds finds."""
+    from icpp_tuning_amd.autotuner import rank_all
+    from icpp_tuning_amd.autotuner.perfdb import TOPK, rescore
+
+    desc = DESCS["gemm_splitk_f16"]
+    shape = {"M": 500, "N": 2304, "K": 768}
+    ranked = [e["formatted"] for e in rank_all(desc, MI355X, **shape)]
+    ms = {n: 10.0 for n in (desc.format_config(r) for r in desc.get_raw_configs(**shape))}
+    ms[ranked[0]], ms[ranked[2]], ms[ranked[7]] = 4.0, 2.0, 1.0      # oracle 1.0 at rank 8
+    row = {"shape": shape, "oracle": ranked[7], "oracle_ms": 1.0, "level": "table", "pick": ranked[7],
+           "pick_ms": 1.0, "pruned_best_ms": 1.0, "ms": ms}
+    rep = rescore(desc, {"rows": [row]}, MI355X)
+    assert rep["rows"][0]["formula_ranking"] == ranked[:max(TOPK)]
+    got = {k: v["perf_ratio_mean"] for k, v in rep["formula_topk"].items()}
+    assert got == {"1": 0.25, "2": 0.25, "4": 0.5, "8": 1.0}
