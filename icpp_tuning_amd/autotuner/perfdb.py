@@ -1,4 +1,4 @@
-"""Offline performance database, decision table and the two-level online select.
+"""Offline performance database, decision table and the three-level online select.
 
 The reference designs this stage but ships no code for it
 (docs/autotuner_design.md:234-268 offline / online split; :457-465
@@ -10,8 +10,10 @@ docstring kernel/autotuner/__init__.py:1-11 names the levels):
            group the measurements by every shape dimension but one axis
            (M for GEMM-family ops, the batch N for conv) and split that axis
            into intervals, each owning the measured-best config -> DecisionTable
+           fit a residual on the schedule model from every record (residual.py)
   online   Level 1: decision-table lookup (profiled shape ranges)
-           Level 2: formula argmax (select_best) for shapes the table misses
+           Level 2: schedule model + learned residual for shapes the table misses
+           Level 3: formula argmax (select_best) without a database
 
 Here "measured best" comes from `tune()` on the device, every candidate it
 measured is kept as a record, and the database is plain JSON (no pickle), keyed
@@ -19,9 +21,10 @@ by the descriptor name and the GPU it was measured on.  Databases profiled on
 MI355X ship in the package (perf_db/mi355x/<name>_<dtype>.json) and are what
 `AdaptiveTuner(descriptor)` loads by default.  `evaluate` measures, on shapes
 that were not profiled, how close each level's pick comes to the exhaustively
-measured best (the reference's accuracy table, docs :529-535).  The reference's
-third level (a LightGBM residual on the formula) has no dependency available
-here and is not built.
+measured best (the reference's accuracy table, docs :529-535); `cross_validate`
+(residual.py) checks the residual level on groups of shapes it was not fitted
+on.  The reference's residual is a LightGBM model; LightGBM is not in this
+image, and the residual here is numpy gradient-boosted trees stored as JSON.
 """
 
 from __future__ import annotations
@@ -33,8 +36,10 @@ from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Any, Dict, Iterable, List, Optional, Sequence, Tuple
 
+from .cost_model import ideal_seconds
 from .gpu_spec import GPUSpec, get_gpu_spec
 from .interface import TileLangKernelBase, rank_all, select_best, tune
+from .residual import ResidualModel, cross_validate, fit_residual
 
 SHIPPED_DIR = Path(__file__).resolve().parents[1] / "perf_db"
 
@@ -140,9 +145,17 @@ class PerformanceDB:
     records: List[ProfileRecord] = field(default_factory=list)
     table: DecisionTable = field(default_factory=DecisionTable)
     created: float = 0.0
+    residual: Optional[Dict[str, Any]] = None    # ResidualModel.as_dict() fitted on `records`
 
     def rebuild(self, axis: Optional[str] = None) -> None:
         self.table = build_decision_table(self.records, axis)
+
+    def fit_residual(self, descriptor: TileLangKernelBase, hw: GPUSpec) -> None:
+        """Fit the second online level's residual model on this database's records."""
+        self.residual = fit_residual(descriptor, self.records, hw).as_dict()
+
+    def residual_model(self) -> Optional[ResidualModel]:
+        return ResidualModel.from_dict(self.residual) if self.residual else None
 
     def to_json(self) -> str:
         """Shapes and configs are pooled once; a record is [shape index, config index, ms]."""
@@ -153,10 +166,12 @@ class PerformanceDB:
             sk = json.dumps(r.shape, sort_keys=True)
             ck = json.dumps(r.config, sort_keys=True)
             rows.append([shapes.setdefault(sk, len(shapes)), configs.setdefault(ck, len(configs)), r.ms])
-        return json.dumps({"op": self.op, "hw": self.hw, "created": self.created,
-                           "shapes": [json.loads(k) for k in shapes], "configs": [json.loads(k) for k in configs],
-                           "records": rows, "table": self.table.as_dict()},
-                          sort_keys=True, separators=(",", ":"))
+        d = {"op": self.op, "hw": self.hw, "created": self.created,
+             "shapes": [json.loads(k) for k in shapes], "configs": [json.loads(k) for k in configs],
+             "records": rows, "table": self.table.as_dict()}
+        if self.residual is not None:
+            d["residual"] = self.residual
+        return json.dumps(d, sort_keys=True, separators=(",", ":"))
 
     @classmethod
     def from_json(cls, text: str) -> "PerformanceDB":
@@ -164,7 +179,7 @@ class PerformanceDB:
         shapes, configs = d["shapes"], d["configs"]
         return cls(op=d["op"], hw=d["hw"], created=d.get("created", 0.0),
                    records=[ProfileRecord(dict(shapes[si]), dict(configs[ci]), float(ms)) for si, ci, ms in d["records"]],
-                   table=DecisionTable.from_dict(d["table"]))
+                   table=DecisionTable.from_dict(d["table"]), residual=d.get("residual"))
 
     def save(self, path) -> None:
         Path(path).write_text(self.to_json())
@@ -250,15 +265,19 @@ def build_db(descriptor: TileLangKernelBase, shapes: Sequence[Dict[str, int]], h
 @dataclass
 class SelectResult:
     config: Dict[str, Any]
-    level: str            # "table" or "formula"
+    level: str            # "table", "residual" or "formula"
     score: Optional[float] = None
     seconds: float = 0.0
 
 
 class AdaptiveTuner:
-    """Two-level online select (reference docs :491-525): decision table, then
-    formula argmax.  A table entry is used only when the descriptor still offers
-    that config for the shape (same compiled set, K / split constraints hold)."""
+    """Three-level online select (reference docs :491-525, levels named in
+    kernel/autotuner/__init__.py:8-11): the decision table for profiled shape
+    ranges; the schedule model corrected by the database's learned residual for
+    shapes the table misses; the formula argmax when there is no database (or it
+    carries no residual).  A table entry is used only when the descriptor still
+    offers that config for the shape (same compiled set, K / split constraints
+    hold).  The residual level ranks the same pruned configs as the formula."""
 
     def __init__(self, descriptor: TileLangKernelBase, db: Any = "auto", hw: Optional[GPUSpec] = None):
         """db: a PerformanceDB, a path to one, "auto" (the database shipped for
@@ -272,6 +291,7 @@ class AdaptiveTuner:
         elif isinstance(db, (str, Path)):
             db = PerformanceDB.load(db)
         self.db = db if (db is None or (db.op == op_key(descriptor) and db.hw == self.hw.name)) else None
+        self.residual = self.db.residual_model() if self.db is not None and self.hw.has_mfma_model else None
 
     def select(self, **shape) -> SelectResult:
         t0 = time.perf_counter()
@@ -279,6 +299,15 @@ class AdaptiveTuner:
             cfg = self.db.table.lookup(shape)
             if cfg is not None and cfg in self.descriptor.get_raw_configs(**shape):
                 return SelectResult(cfg, "table", None, time.perf_counter() - t0)
+        if self.residual is not None:
+            raws = self.descriptor.prune(self.descriptor.get_raw_configs(**shape), self.hw, **shape)
+            if raws:
+                lt = self.residual.log_time(self.descriptor, raws, self.hw, shape)
+                best = int(lt.argmin())
+                cfg = raws[best]
+                op = self.descriptor.make_op_spec(raw_config=cfg, **shape)
+                score = ideal_seconds(op, self.descriptor.raw_config_to_tune_config(cfg), self.hw) / math.exp(lt[best])
+                return SelectResult(cfg, "residual", score, time.perf_counter() - t0)
         cfg, score = select_best(self.descriptor, self.hw, **shape)
         return SelectResult(cfg, "formula", score, time.perf_counter() - t0)
 
@@ -440,8 +469,9 @@ def _descriptors():
 
 
 def main(argv=None) -> int:  # pragma: no cover - device tool
-    """Offline builder (reference docs :539-553): profile, build the table,
-    write the JSON, and optionally evaluate both levels on held-out shapes."""
+    """Offline builder (reference docs :539-553): profile, build the table, fit
+    the residual, write the JSON, and optionally evaluate the levels on held-out
+    shapes."""
     import argparse
 
     ops = _descriptors()
@@ -454,9 +484,27 @@ def main(argv=None) -> int:  # pragma: no cover - device tool
     ap.add_argument("--eval-only", action="store_true", help="evaluate the database at --out (or the shipped one)")
     ap.add_argument("--rescore", default="", help="an --eval-out report: re-pick its formula column with the "
                     "current cost model against the times it holds (no device work), write to --eval-out")
+    ap.add_argument("--fit-residual", action="store_true",
+                    help="fit the residual level on the database at --out (or the shipped one) and save it there")
+    ap.add_argument("--cv-residual", default="", help="leave-one-group-out check of the residual level on the "
+                    "database at --out (or the shipped one); write the report to this path")
     a = ap.parse_args(argv)
     desc = ops[a.op]
     hw = get_gpu_spec()
+    if a.fit_residual or a.cv_residual:
+        path = Path(a.out) if a.out else shipped_path(op_key(desc), hw)
+        db = PerformanceDB.load(path)
+        if a.cv_residual:
+            axis = db.table.axis
+            rows = cross_validate(desc, db.records, hw, lambda s: _group_key(s, axis))
+            Path(a.cv_residual).write_text(json.dumps({"op": op_key(desc), "groups": rows}, indent=1))
+            for r in rows:
+                print(json.dumps(r), flush=True)
+        if a.fit_residual:
+            db.fit_residual(desc, hw)
+            db.save(path)
+            print(f"[perfdb] residual fitted on {len(db.records)} records -> {path}", flush=True)
+        return 0
     if a.rescore:
         rep = rescore(desc, json.loads(Path(a.rescore).read_text()), hw)
         if a.eval_out:
@@ -471,6 +519,7 @@ def main(argv=None) -> int:  # pragma: no cover - device tool
     else:
         print(f"[perfdb] {a.op}: {len(shapes)} shapes", flush=True)
         db = build_db(desc, shapes, hw, top_k=a.top_k, budget_ms=a.budget_ms, log=lambda m: print(m, flush=True))
+        db.fit_residual(desc, hw)
         out.parent.mkdir(parents=True, exist_ok=True)
         db.save(out)
         print(f"[perfdb] {len(db.records)} records, {sum(len(v) for v in db.table.groups.values())} intervals -> "
