@@ -355,14 +355,15 @@ def evaluate(descriptor: TileLangKernelBase, db: Optional[PerformanceDB], shapes
         ranked = _formula_ranking(descriptor, hw, shape)
         formula = ranked[0]
         pick = descriptor.format_config(sel.config)
-        row = {"shape": dict(shape), "oracle": descriptor.format_config(res.best_config), "oracle_ms": res.best_ms,
+        oracle = min(ms, key=ms.get)       # from the same single timings as every pick it is compared with
+        row = {"shape": dict(shape), "oracle": oracle, "oracle_ms": ms[oracle],
                "level": sel.level, "pick": pick, "pick_ms": ms.get(pick), "formula": formula,
                "formula_ms": ms[formula], "formula_ranking": ranked,
                "pruned_best_ms": min(v for k, v in ms.items() if k in kept),
                "n_measured": len(ms), "n_pruned_set": len(kept), "ms": ms}
         rows.append(row)
         if log:
-            log(f"[perfdb-eval] {descriptor.name} {shape}: oracle {row['oracle']} {res.best_ms * 1e3:.1f} us, "
+            log(f"[perfdb-eval] {descriptor.name} {shape}: oracle {oracle} {ms[oracle] * 1e3:.1f} us, "
                 f"{sel.level} {pick} {(row['pick_ms'] or float('nan')) * 1e3:.1f} us, formula {formula} "
                 f"{row['formula_ms'] * 1e3:.1f} us")
     return _report(descriptor, rows)
@@ -371,13 +372,17 @@ def evaluate(descriptor: TileLangKernelBase, db: Optional[PerformanceDB], shapes
 def rescore(descriptor: TileLangKernelBase, report: Dict[str, Any], hw: Optional[GPUSpec] = None) -> Dict[str, Any]:
     """Re-pick the formula's top-1 of every row of an `evaluate` report with the
     current cost model and score it against the times the row already holds
-    (every compiled config was measured there): no device work."""
+    (every compiled config was measured there): no device work.  The oracle is
+    the fastest of those times (reports written before that rule took the
+    tuner's re-timed best)."""
     hw = hw or get_gpu_spec()
     rows = []
     for r in report["rows"]:
         ranked = _formula_ranking(descriptor, hw, r["shape"])
         formula = ranked[0]
-        row = dict(r, formula=formula, formula_ms=r["ms"][formula], formula_ranking=ranked)
+        oracle = min(r["ms"], key=r["ms"].get)
+        row = dict(r, oracle=oracle, oracle_ms=r["ms"][oracle], formula=formula, formula_ms=r["ms"][formula],
+                   formula_ranking=ranked)
         if r["level"] == "formula":      # a table miss falls back to the formula's pick
             row.update(pick=formula, pick_ms=r["ms"][formula])
         rows.append(row)
@@ -459,6 +464,24 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
                                points_per_wave=2)
 
 
+def unseen_plan(op: str) -> List[Dict[str, int]]:
+    """Shapes in groups the shipped databases never profiled -- other (N, K)
+    pairs, other conv geometries -- where the table always misses: what the
+    residual level is for."""
+    if op == "conv2d" or op.startswith("conv2d_") or op == "conv_bn_add_relu":
+        geos = [dict(C=128, H=28, W=28, OC=128, KH=3, KW=3, stride=1, padding=1),
+                dict(C=256, H=28, W=28, OC=256, KH=3, KW=3, stride=1, padding=1)]
+        return [dict(g, N=b) for g in geos for b in (4, 16, 48)]
+    grid = {
+        "gemm_splitk": ([(1536, 3072), (3072, 1536), (6144, 2048)], (48, 700, 2500)),
+        "fp8_gemm_bias_silu": ([(8192, 8192), (14336, 4096), (4096, 14336)], (32, 512, 2048)),
+        "gemm_bias_layernorm": ([(512, 1024), (2048, 2048)], (1000, 4000)),
+        "gemm_bias_gelu_erf": ([(2048, 512), (5120, 1280)], (512, 4000)),
+    }
+    nk, ms = grid.get(op, ([(3072, 768), (8192, 2048), (2048, 8192)], (256, 1500, 6000)))
+    return [dict(M=m, N=n, K=k) for n, k in nk for m in ms]
+
+
 def _descriptors():
     from ..kernels import conv2d, conv2d_fused, fp8_gemm_bias_act, gemm, gemm_bias_act, gemm_bias_layernorm
 
@@ -484,6 +507,8 @@ def main(argv=None) -> int:  # pragma: no cover - device tool
     ap.add_argument("--eval-only", action="store_true", help="evaluate the database at --out (or the shipped one)")
     ap.add_argument("--rescore", default="", help="an --eval-out report: re-pick its formula column with the "
                     "current cost model against the times it holds (no device work), write to --eval-out")
+    ap.add_argument("--eval-unseen", default="", help="evaluate the database at --out (or the shipped one) on "
+                    "shapes of groups it never profiled (unseen_plan); write the report to this path")
     ap.add_argument("--fit-residual", action="store_true",
                     help="fit the residual level on the database at --out (or the shipped one) and save it there")
     ap.add_argument("--cv-residual", default="", help="leave-one-group-out check of the residual level on the "
@@ -514,6 +539,11 @@ def main(argv=None) -> int:  # pragma: no cover - device tool
         return 0
     shapes = default_plan(a.op, hw)
     out = Path(a.out) if a.out else shipped_path(op_key(desc), hw)
+    if a.eval_unseen:
+        rep = evaluate(desc, PerformanceDB.load(out), unseen_plan(a.op), hw, log=lambda m: print(m, flush=True))
+        Path(a.eval_unseen).write_text(json.dumps(rep, indent=1))
+        print(json.dumps({k: rep[k] for k in ("op", "formula", "formula_topk", "combined", "pruned_set")}), flush=True)
+        return 0
     if a.eval_only:
         db = PerformanceDB.load(out)
     else:
@@ -537,4 +567,4 @@ if __name__ == "__main__":  # pragma: no cover
 
 __all__ = ["AdaptiveTuner", "DecisionTable", "PerformanceDB", "ProfileRecord", "SelectResult", "build_db",
            "build_decision_table", "build_sampling_plan", "default_axis", "default_plan", "evaluate", "held_out",
-           "op_key", "profile", "select_config", "shipped_path"]
+           "op_key", "profile", "rescore", "select_config", "shipped_path", "unseen_plan"]

@@ -118,3 +118,19 @@ def test_cross_validate_reports_every_group():
     for r in rows:
         for k in ("formula_mean", "formula_min", "residual_mean", "residual_min"):
             assert 0.0 < r[k] <= 1.0
+
+
+@pytest.mark.parametrize("key", sorted(DESCS))
+def test_unseen_plan_misses_the_table(key):
+    """`perfdb --eval-unseen` measures the residual level: every shape of its
+    plan lies in a group the shipped database never profiled."""
+    from icpp_tuning_amd.autotuner.perfdb import unseen_plan
+
+    desc = DESCS[key]
+    db = PerformanceDB.load(shipped_path(key, MI355X))
+    profiled = {_group_key(r.shape, db.table.axis) for r in db.records}
+    t = AdaptiveTuner(desc, db, MI355X)
+    for shape in unseen_plan(desc.name):
+        assert _group_key(shape, db.table.axis) not in profiled
+        assert desc.get_raw_configs(**shape)
+        assert t.select(**shape).level == "residual"
