@@ -151,8 +151,9 @@ class PerformanceDB:
         self.table = build_decision_table(self.records, axis)
 
     def fit_residual(self, descriptor: TileLangKernelBase, hw: GPUSpec) -> None:
-        """Fit the second online level's residual model on this database's records."""
-        self.residual = fit_residual(descriptor, self.records, hw).as_dict()
+        """Fit the second online level's residual model on this database's records
+        (none without records)."""
+        self.residual = fit_residual(descriptor, self.records, hw).as_dict() if self.records else None
 
     def residual_model(self) -> Optional[ResidualModel]:
         return ResidualModel.from_dict(self.residual) if self.residual else None
