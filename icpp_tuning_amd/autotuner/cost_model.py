@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
-from typing import Dict, Iterable, List, Literal, Optional, Sequence, Tuple
+from typing import Any, Dict, Iterable, List, Literal, Optional, Sequence, Tuple
 
 from .gpu_spec import GPUSpec
 
@@ -680,7 +680,7 @@ def ideal_seconds(op: OpSpec, config: TuneConfig, hw: GPUSpec) -> float:
 
 
 def predict_schedule(op: OpSpec, config: TuneConfig, hw: GPUSpec,
-                     c: Optional[ModelConstants] = None) -> Dict[str, float]:
+                     c: Optional[ModelConstants] = None) -> Dict[str, Any]:
     """Predicted time of one launch on a CDNA4 device, in seconds.
 
     Workgroups are spread evenly over the CUs: the busiest CU runs
@@ -689,7 +689,8 @@ def predict_schedule(op: OpSpec, config: TuneConfig, hw: GPUSpec,
     One K step of one workgroup needs
 
       MFMA   (BM/m)(BN/n)(BK/k) issue cycles / sustained rate, spread over
-             min(4, waves on the CU) SIMDs,
+             the waves, which sit on the 4 SIMDs round-robin: the busiest
+             SIMD issues for ceil(waves on the CU / 4) of them,
       LDS    every wave reads its A rows and B columns, and the tile is
              written once: (waves (WTM + WTN) + BM + BN) BK bytes at
              ``hw.lds_bytes_per_clk``,
@@ -722,7 +723,6 @@ def predict_schedule(op: OpSpec, config: TuneConfig, hw: GPUSpec,
     else:   # no MFMA shape: the dtype's dense peak per SIMD
         per_simd = hw.peak_tflops(op.mainloop.dtype) * 1e12 / (hw.num_sm * simds * clk)
         issue = op.mainloop.flops_per_fma * config.block_M * config.block_N * config.block_K / per_simd
-    # waves sit on SIMDs round-robin: the busiest SIMD holds ceil(waves / 4)
     mfma_shared = _ceildiv(conc * waves, simds) * issue / (waves * conc)
     mfma_alone = _ceildiv(waves, simds) * issue / waves
     wm, wn = config.wave_grid()
