@@ -152,7 +152,7 @@ class TuneResult:
     best_config: Dict[str, Any]
     best_ms: float
     best_tflops: float
-    formula_top1: Dict[str, Any]
+    formula_top1: Dict[str, Any]        # the ranking's first config: the formula's, unless `ranked` was given
     formula_top1_ms: float
     candidates: List[Dict[str, Any]] = field(default_factory=list)
     prune_rank_s: float = 0.0
@@ -225,7 +225,8 @@ def input_bytes(inputs: Any) -> int:
 
 def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: int = 4, warmup: int = 2,
          reps: int = 5, budget_ms: float = 0.0, prune: bool = True, input_copies: Union[int, str] = 1,
-         seed_configs: Sequence[Dict[str, Any]] = (), **shape_kwargs: Any) -> TuneResult:
+         seed_configs: Sequence[Dict[str, Any]] = (), ranked: Optional[Sequence[Dict[str, Any]]] = None,
+         **shape_kwargs: Any) -> TuneResult:
     """Formula-rank, then measure candidates on the device and keep the fastest.
 
     The formula's top_k are always measured.  With ``budget_ms`` the search goes
@@ -237,7 +238,10 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     of a search is discarded (it absorbs the clock ramp-up of an idle device),
     and the two fastest candidates are timed again and ranked on the mean.
     ``prune=False`` ranks (and, with a large top_k, measures) the whole compiled
-    set for the shape, as offline profiling does.  ``input_copies`` > 1 times
+    set for the shape, as offline profiling does.  ``ranked`` replaces the
+    formula's ranking with another one in `rank_all`'s form (e.g.
+    `AdaptiveTuner.rank`, which corrects the formula with a database's
+    learned residual).  ``input_copies`` > 1 times
     every candidate round-robin over that many input sets, so an operand set
     that would otherwise stay resident in the 256 MiB MALL is read from HBM on
     every launch -- the condition a memory-bound op is judged in; "auto" picks
@@ -251,7 +255,7 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
     if hw is None:
         hw = get_gpu_spec()
     all_cfgs = descriptor.get_raw_configs(**shape_kwargs)
-    ranked = rank_all(descriptor, hw, prune=prune, **shape_kwargs)
+    ranked = list(ranked) if ranked is not None else rank_all(descriptor, hw, prune=prune, **shape_kwargs)
     if not ranked:
         raise RuntimeError(f"No configs survive pruning for {descriptor.name} with {shape_kwargs}")
     t1 = time.perf_counter()

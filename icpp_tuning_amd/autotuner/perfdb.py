@@ -301,16 +301,27 @@ class AdaptiveTuner:
             if cfg is not None and cfg in self.descriptor.get_raw_configs(**shape):
                 return SelectResult(cfg, "table", None, time.perf_counter() - t0)
         if self.residual is not None:
-            raws = self.descriptor.prune(self.descriptor.get_raw_configs(**shape), self.hw, **shape)
-            if raws:
-                lt = self.residual.log_time(self.descriptor, raws, self.hw, shape)
-                best = int(lt.argmin())
-                cfg = raws[best]
-                op = self.descriptor.make_op_spec(raw_config=cfg, **shape)
-                score = ideal_seconds(op, self.descriptor.raw_config_to_tune_config(cfg), self.hw) / math.exp(lt[best])
-                return SelectResult(cfg, "residual", score, time.perf_counter() - t0)
+            ranked = self.rank(**shape)
+            if ranked:
+                return SelectResult(ranked[0]["raw_config"], "residual", ranked[0]["score"], time.perf_counter() - t0)
         cfg, score = select_best(self.descriptor, self.hw, **shape)
         return SelectResult(cfg, "formula", score, time.perf_counter() - t0)
+
+    def rank(self, **shape) -> List[Dict[str, Any]]:
+        """The pruned configs best first, in `rank_all`'s form, by the formula
+        corrected with the database's residual when there is one (the order the
+        residual level picks from), else by the formula.  For `tune(ranked=...)`."""
+        if self.residual is None:
+            return rank_all(self.descriptor, self.hw, **shape)
+        raws = self.descriptor.prune(self.descriptor.get_raw_configs(**shape), self.hw, **shape)
+        lt = self.residual.log_time(self.descriptor, raws, self.hw, shape)
+        out = []
+        for i in sorted(range(len(raws)), key=lambda i: lt[i]):
+            op = self.descriptor.make_op_spec(raw_config=raws[i], **shape)
+            ideal = ideal_seconds(op, self.descriptor.raw_config_to_tune_config(raws[i]), self.hw)
+            out.append({"raw_config": raws[i], "score": ideal / math.exp(lt[i]),
+                        "formatted": self.descriptor.format_config(raws[i])})
+        return out
 
     def precompile(self) -> Dict[str, int]:
         """Reference `precompile_top_configs` (docs :482-484).  Kernels here are

@@ -105,3 +105,16 @@ def test_failing_candidate_is_dropped_with_its_reason(monkeypatch, fake_device):
     monkeypatch.setattr(d, "make_runner", lambda raw, inp, **shape: (_ for _ in ()).throw(ValueError("no")))
     with pytest.raises(RuntimeError, match="every measured candidate failed"):
         tune(d, MI355X, top_k=2, **SHAPE)
+
+
+def test_given_ranking_replaces_the_formula(fake_device):
+    """tune(ranked=...) measures down the given order (e.g. AdaptiveTuner.rank)."""
+    from icpp_tuning_amd.autotuner.perfdb import AdaptiveTuner
+
+    d = fake_device
+    order = AdaptiveTuner(d, hw=MI355X).rank(**SHAPE)
+    assert {e["formatted"] for e in order} == {e["formatted"] for e in rank_all(d, MI355X, **SHAPE)}
+    reverse = order[::-1]
+    r = tune(d, MI355X, top_k=3, ranked=reverse, **SHAPE)
+    assert [c["config"] for c in r.candidates] == [e["raw_config"] for e in reverse[:3]]
+    assert r.formula_top1 == reverse[0]["raw_config"]
