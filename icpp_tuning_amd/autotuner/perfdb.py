@@ -293,8 +293,24 @@ class AdaptiveTuner:
             db = PerformanceDB.load(db)
         self.db = db if (db is None or (db.op == op_key(descriptor) and db.hw == self.hw.name)) else None
         self.residual = self.db.residual_model() if self.db is not None and self.hw.has_mfma_model else None
+        self._memo: Dict[str, SelectResult] = {}
+
+    MEMO_MAX = 4096
 
     def select(self, **shape) -> SelectResult:
+        """The answers are memoised per shape (at most MEMO_MAX shapes), so a
+        process that meets the same shapes again pays the residual level once."""
+        t0 = time.perf_counter()
+        key = json.dumps(shape, sort_keys=True)
+        hit = self._memo.get(key)
+        if hit is None:
+            hit = self._select(shape)
+            if len(self._memo) >= self.MEMO_MAX:
+                self._memo.clear()
+            self._memo[key] = hit
+        return SelectResult(dict(hit.config), hit.level, hit.score, time.perf_counter() - t0)
+
+    def _select(self, shape: Dict[str, Any]) -> SelectResult:
         t0 = time.perf_counter()
         if self.db is not None:
             cfg = self.db.table.lookup(shape)

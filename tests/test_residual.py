@@ -134,3 +134,17 @@ def test_unseen_plan_misses_the_table(key):
         assert _group_key(shape, db.table.axis) not in profiled
         assert desc.get_raw_configs(**shape)
         assert t.select(**shape).level == "residual"
+
+
+def test_select_is_memoised_per_shape():
+    desc = DESCS["gemm_bias_gelu_tanh_bf16"]
+    t = AdaptiveTuner(desc, hw=MI355X)
+    unseen = {"M": 3000, "N": 2048, "K": 2560}
+    a = t.select(**unseen)
+    a.config["block_M"] = -1                      # a caller's change does not reach the memo
+    b = t.select(**unseen)
+    assert b.level == "residual" and b.config["block_M"] > 0
+    assert b.seconds < 1e-3
+    t.MEMO_MAX = 1
+    t.select(M=3001, N=2048, K=2560)
+    assert len(t._memo) == 1
