@@ -482,13 +482,15 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
     if op == "fp8_gemm_bias_silu":
         return build_sampling_plan(op, hw, m_range=(16, 4096), nk=[(4096, 4096), (11008, 4096), (4096, 11008)],
                                    points_per_wave=2)
-    if op == "gemm_bias_layernorm":   # C3 shapes, plus BERT-base's attention-output and FFN-output blocks
+    if op == "gemm_bias_layernorm":   # C3 shapes, BERT-base's attention-output and FFN-output blocks, and the
+        # reference's evaluation shape (N = 2304, K = 768: gemm_three_ops_formula_summary.csv)
         return build_sampling_plan(op, hw, m_range=(128, 8192),
-                                   nk=[(768, 4096), (1024, 4096), (4096, 4096), (768, 768), (768, 3072)],
+                                   nk=[(768, 4096), (1024, 4096), (4096, 4096), (768, 768), (768, 3072), (2304, 768)],
                                    points_per_wave=2)
     if op == "gemm_bias_gelu_erf":     # BERT-base's FFN-in block (end2end.py:82-83)
         return build_sampling_plan(op, hw, m_range=(128, 16384), nk=[(3072, 768), (4096, 1024)], points_per_wave=2)
-    return build_sampling_plan(op, hw, m_range=(16, 8192), nk=[(4096, 4096), (1024, 4096), (4096, 1024)],
+    # GEMM + bias + activation: C2's 4096-class shapes and the reference's evaluation shape
+    return build_sampling_plan(op, hw, m_range=(16, 8192), nk=[(4096, 4096), (1024, 4096), (4096, 1024), (2304, 768)],
                                points_per_wave=2)
 
 
@@ -513,7 +515,8 @@ def unseen_plan(op: str) -> List[Dict[str, int]]:
 def _descriptors():
     from ..kernels import conv2d, conv2d_fused, fp8_gemm_bias_act, gemm, gemm_bias_act, gemm_bias_layernorm
 
-    ds = [gemm.DESCRIPTOR, gemm_bias_act.descriptor("gelu_tanh", "bf16"), gemm_bias_act.descriptor("gelu_erf", "f16"),
+    ds = [gemm.DESCRIPTOR, gemm_bias_act.descriptor("gelu_tanh", "bf16"), gemm_bias_act.descriptor("relu", "bf16"),
+          gemm_bias_act.descriptor("silu", "bf16"), gemm_bias_act.descriptor("gelu_erf", "f16"),
           gemm_bias_layernorm.DESCRIPTOR, fp8_gemm_bias_act.DESCRIPTOR, conv2d.DESCRIPTOR] + \
         list(conv2d_fused.DESCRIPTORS.values())
     return {d.name: d for d in ds}
