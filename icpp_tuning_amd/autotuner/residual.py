@@ -244,23 +244,22 @@ def cross_validate(descriptor, records, hw: GPUSpec, group_of, **kw) -> List[Dic
     by: Dict[str, list] = {}
     for r in records:
         by.setdefault(json.dumps(r.shape, sort_keys=True), []).append(r)
-    shapes = [json.loads(k) for k in by]
-    groups = [group_of(s) for s in shapes]
+    keys = list(by)                      # the shape order of training_set's ids
+    groups = [group_of(json.loads(k)) for k in keys]
     out = []
     for g in sorted(set(groups)):
         train = np.array([groups[i] != g for i in gid])
         model = fit_boosted_trees(X[train], y[train], **kw)
         ratios: Dict[str, List[float]] = {"formula": [], "residual": []}
-        for i, shape in enumerate(shapes):
+        for i, key in enumerate(keys):
             if groups[i] != g:
                 continue
-            rows = gid == i
-            ms = np.array([r.ms for r in by[json.dumps(shape, sort_keys=True)]])
-            kept = {descriptor.format_config(c) for c in descriptor.prune(descriptor.get_raw_configs(**shape), hw,
-                                                                          **shape)}
-            ok = np.array([descriptor.format_config(r.config) in kept
-                           for r in by[json.dumps(shape, sort_keys=True)]])
-            names = [descriptor.format_config(r.config) for r in by[json.dumps(shape, sort_keys=True)]]
+            shape, recs, rows = json.loads(key), by[key], gid == i
+            ms = np.array([r.ms for r in recs])
+            names = [descriptor.format_config(r.config) for r in recs]
+            kept = {descriptor.format_config(c)
+                    for c in descriptor.prune(descriptor.get_raw_configs(**shape), hw, **shape)}
+            ok = np.array([n in kept for n in names])
             formula = names.index(descriptor.format_config(select_best(descriptor, hw, **shape)[0]))
             corrected = np.where(ok, X[rows, 0] + model.predict(X[rows]), np.inf)
             ratios["formula"].append(float(ms.min() / ms[formula]))
