@@ -472,9 +472,15 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
     """The shapes the shipped databases were profiled on."""
     hw = hw or get_gpu_spec()
     if op == "conv2d" or op.startswith("conv2d_") or op == "conv_bn_add_relu":
+        # the three C4 geometries, then ResNet-50's other kinds of layer: the 28^2 stage's
+        # 3x3, a stride-2 3x3, and two 1x1 bottleneck projections
         geos = [dict(C=64, H=56, W=56, OC=64, KH=3, KW=3, stride=1, padding=1),
                 dict(C=256, H=14, W=14, OC=256, KH=3, KW=3, stride=1, padding=1),
-                dict(C=512, H=7, W=7, OC=512, KH=3, KW=3, stride=1, padding=1)]
+                dict(C=512, H=7, W=7, OC=512, KH=3, KW=3, stride=1, padding=1),
+                dict(C=128, H=28, W=28, OC=128, KH=3, KW=3, stride=1, padding=1),
+                dict(C=128, H=56, W=56, OC=128, KH=3, KW=3, stride=2, padding=1),
+                dict(C=256, H=56, W=56, OC=64, KH=1, KW=1, stride=1, padding=0),
+                dict(C=1024, H=14, W=14, OC=256, KH=1, KW=1, stride=1, padding=0)]
         return build_sampling_plan("conv2d", hw, conv=geos, batches=(1, 2, 4, 8, 16, 32, 48, 64, 128))
     if op == "gemm_splitk":   # the reference's offline-builder example (docs :543-549)
         nk = [(n, k) for n in (768, 2304, 4096) for k in (768, 2304, 4096)]
@@ -499,8 +505,9 @@ def unseen_plan(op: str) -> List[Dict[str, int]]:
     pairs, other conv geometries -- where the table always misses: what the
     residual level is for."""
     if op == "conv2d" or op.startswith("conv2d_") or op == "conv_bn_add_relu":
-        geos = [dict(C=128, H=28, W=28, OC=128, KH=3, KW=3, stride=1, padding=1),
-                dict(C=256, H=28, W=28, OC=256, KH=3, KW=3, stride=1, padding=1)]
+        geos = [dict(C=192, H=28, W=28, OC=192, KH=3, KW=3, stride=1, padding=1),
+                dict(C=256, H=28, W=28, OC=256, KH=3, KW=3, stride=1, padding=1),
+                dict(C=512, H=28, W=28, OC=128, KH=1, KW=1, stride=1, padding=0)]
         return [dict(g, N=b) for g in geos for b in (4, 16, 48)]
     grid = {
         "gemm_splitk": ([(1536, 3072), (3072, 1536), (6144, 2048)], (48, 700, 2500)),

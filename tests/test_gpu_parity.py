@@ -291,12 +291,13 @@ def test_conv_geometries(gpu, geom):
     ref = O.conv2d_nhwc_ref(d["X"], d["W"], S, P, D)
     X, Wt = d["X"].cuda(), d["W"].cuda()
     for idx, inst in enumerate(family_instances("conv2d")):
-        if (KH * KW * C) % inst.bk:
-            continue
-        raw = raw_from_inst(inst, 1)
-        print(f"[parity] conv {geom} {inst.name}", flush=True)
-        k = conv_mod.build_conv2d_kernel(Nb, C, H, W, F, KH, KW, S, P, D, config=raw)
-        Y = torch.full(tuple(ref.shape), float("nan"), dtype=torch.float16, device="cuda")
-        k(X, Wt, Y)
-        torch.cuda.synchronize()
-        _close(Y, ref, 1e-2, 1e-2, f"conv {geom} {inst.name}")
+        for sk in (1, 2):          # split-K slices the same gathers at a K offset
+            if (KH * KW * C) % (inst.bk * sk):
+                continue
+            raw = raw_from_inst(inst, sk)
+            print(f"[parity] conv {geom} {inst.name} sk={sk}", flush=True)
+            k = conv_mod.build_conv2d_kernel(Nb, C, H, W, F, KH, KW, S, P, D, config=raw)
+            Y = torch.full(tuple(ref.shape), float("nan"), dtype=torch.float16, device="cuda")
+            k(X, Wt, Y)
+            torch.cuda.synchronize()
+            _close(Y, ref, 1e-2, 1e-2, f"conv {geom} {inst.name} sk={sk}")
