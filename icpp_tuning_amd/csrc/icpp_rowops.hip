@@ -95,6 +95,32 @@ __device__ __forceinline__ float row_reduce(float v, Op op, int tpr, float (*red
   return r;
 }
 
+// Two row sums behind one workgroup barrier, each summed in row_reduce's order.
+// The two pair buffers alternate like row_reduce's slots: the next pair's writes
+// cannot overtake a slow wave still reading this one, because the barrier of the
+// pair in between lies between them.
+__device__ __forceinline__ void row_reduce2(float& a, float& b, int tpr, float (*red)[2][MAX_WAVES], int& slot) {
+  a = wave_reduce(a, Sum{});
+  b = wave_reduce(b, Sum{});
+  if (tpr <= 64) return;
+  const int wave = threadIdx.x >> 6;
+  const int wpr = tpr >> 6;                // waves per row
+  const int first = (wave / wpr) * wpr;    // first wave of this row
+  if ((threadIdx.x & 63) == 0) {
+    red[slot][0][wave] = a;
+    red[slot][1][wave] = b;
+  }
+  __syncthreads();
+  float ra = red[slot][0][first], rb = red[slot][1][first];
+  for (int w = 1; w < wpr; ++w) {
+    ra += red[slot][0][first + w];
+    rb += red[slot][1][first + w];
+  }
+  slot ^= 1;
+  a = ra;
+  b = rb;
+}
+
 // ---------------------------------------------------------------------------
 // LayerNorm forward: y = (x - mean) * rstd * w + b, mean / rstd (fp32) per row
 // (reference _layer_norm_fwd_fused: centred two-pass variance, rstd = 1/sqrt(var+eps)).
@@ -267,7 +293,7 @@ layernorm_bwd_kernel(const T* __restrict__ DY, const T* __restrict__ X, const T*
                      float* __restrict__ part, int M, int N, int ld, int tpr) {
   typedef Chunk<T, VEC> Ch;
   typedef typename Ch::raw Raw;
-  __shared__ float red[2][MAX_WAVES];
+  __shared__ float red[2][2][MAX_WAVES];
   __shared__ f32x4 fold[BWD_BLOCK];  // row-slot folding, one 16-byte value per thread
   int slot = 0;
   const int rpb = blockDim.x / tpr;
@@ -334,8 +360,9 @@ layernorm_bwd_kernel(const T* __restrict__ DY, const T* __restrict__ X, const T*
         s2 += wdy;
       }
     }
-    const float c1 = row_reduce(s1, Sum{}, tpr, red, slot) * inv_n;
-    const float c2 = row_reduce(s2, Sum{}, tpr, red, slot) * inv_n;
+    row_reduce2(s1, s2, tpr, red, slot);
+    const float c1 = s1 * inv_n;
+    const float c2 = s2 * inv_n;
     if (live) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
@@ -393,7 +420,7 @@ __global__ void __launch_bounds__(BWD_BLOCK)
 layernorm_bwd_kernel_long(const T* __restrict__ DY, const T* __restrict__ X, const T* __restrict__ W,
                      const float* __restrict__ mean_in, const float* __restrict__ rstd_in, T* __restrict__ DX,
                      float* __restrict__ part, int M, int N, int ld, int tpr) {
-  __shared__ float red[2][MAX_WAVES];
+  __shared__ float red[2][2][MAX_WAVES];
   __shared__ f32x4 fold[BWD_BLOCK];  // row-slot folding, one 16-byte value per thread
   int slot = 0;
   const int rpb = blockDim.x / tpr;
@@ -441,8 +468,9 @@ layernorm_bwd_kernel_long(const T* __restrict__ DY, const T* __restrict__ X, con
         s2 += wdy[i][e];
       }
     }
-    const float c1 = row_reduce(s1, Sum{}, tpr, red, slot) * inv_n;
-    const float c2 = row_reduce(s2, Sum{}, tpr, red, slot) * inv_n;
+    row_reduce2(s1, s2, tpr, red, slot);
+    const float c1 = s1 * inv_n;
+    const float c2 = s2 * inv_n;
     if (live) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
