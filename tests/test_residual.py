@@ -148,3 +148,24 @@ def test_select_is_memoised_per_shape():
     t.MEMO_MAX = 1
     t.select(M=3001, N=2048, K=2560)
     assert len(t._memo) == 1
+
+
+def test_cli_fit_and_cross_validate(tmp_path):
+    """`perfdb --fit-residual` stores the fit in the database at --out;
+    `--cv-residual` writes one report row per group."""
+
+    from icpp_tuning_amd.autotuner.perfdb import main
+
+    key = "gemm_bias_gelu_erf_f16"
+    path = tmp_path / "db.json"
+    db = PerformanceDB.load(shipped_path(key, MI355X))
+    db.residual = None
+    db.save(path)
+    assert main(["--op", "gemm_bias_gelu_erf", "--out", str(path), "--fit-residual"]) == 0
+    fitted = PerformanceDB.load(path)
+    assert fitted.residual == PerformanceDB.load(shipped_path(key, MI355X)).residual
+    assert [r.as_dict() for r in fitted.records] == [r.as_dict() for r in db.records]
+    report = tmp_path / "cv.json"
+    assert main(["--op", "gemm_bias_gelu_erf", "--out", str(path), "--cv-residual", str(report)]) == 0
+    rep = json.loads(report.read_text())
+    assert rep["op"] == key and len(rep["groups"]) == len({_group_key(r.shape, db.table.axis) for r in db.records})
