@@ -153,7 +153,6 @@ def test_select_is_memoised_per_shape():
 def test_cli_fit_and_cross_validate(tmp_path):
     """`perfdb --fit-residual` stores the fit in the database at --out;
     `--cv-residual` writes one report row per group."""
-
     from icpp_tuning_amd.autotuner.perfdb import main
 
     key = "gemm_bias_gelu_erf_f16"
