@@ -542,6 +542,53 @@ def vs_libraries():
     return rows
 
 
+def reference_eval():
+    """The reference's own evaluation sweep (evaluation/gemm_three_ops_formula_summary.csv:
+    gemm, gemm_bias_act (ReLU), gemm_bias_layernorm at M = 1, 6, ..., 126, N = 2304,
+    K = 768, fp16 in): the config the reference's `build_kernel(config=None)` analogue
+    picks without measuring anything (`select_config`: table, residual or formula
+    level), against the op composed from torch calls, both timed over the same
+    rotated input copies (larger than the MALL)."""
+    import torch
+    import torch.nn.functional as F
+
+    from icpp_tuning_amd.autotuner.interface import benchmark_ms, input_bytes
+    from icpp_tuning_amd.autotuner.perfdb import AdaptiveTuner
+    from icpp_tuning_amd.kernels import gemm as G
+    from icpp_tuning_amd.kernels import gemm_bias_act as GBA
+    from icpp_tuning_amd.kernels import gemm_bias_layernorm as LN
+
+    ops = [("gemm", G.DESCRIPTOR, "mm", lambda d: torch.mm(d["A"], d["B"], out=d["C"])),
+           ("gemm_bias_act", GBA.descriptor("relu", "f16"), "relu(addmm)",
+            lambda d: F.relu(torch.addmm(d["bias"], d["A"], d["B"]))),
+           ("gemm_bias_layernorm", LN.DESCRIPTOR, "layer_norm(addmm)",
+            lambda d: F.layer_norm(torch.addmm(d["bias"], d["A"], d["B"]), (d["B"].shape[1],), d["gamma"],
+                                   d["beta"]))]
+    rows = []
+    for name, desc, torch_name, torch_fn in ops:
+        tuner = AdaptiveTuner(desc)
+        for M in range(1, 127, 5):
+            shape = dict(M=M, N=2304, K=768)
+            sel = tuner.select(**shape)
+            sets = [desc.make_inputs(**shape)]
+            copies = max(1, min(16, -(-(600 << 20) // max(1, input_bytes(sets[0])))))
+            sets += [desc.make_inputs(**shape) for _ in range(copies - 1)]
+            runs = [desc.make_runner(sel.config, d, **shape) for d in sets]
+            reps = max(20, 2 * copies)
+            benchmark_ms(runs, warmup=copies, reps=reps)  # settles the clock after the idle input build
+            ours = benchmark_ms(runs, warmup=copies, reps=reps)
+            t = benchmark_ms([(lambda d=d: torch_fn(d)) for d in sets], warmup=copies, reps=reps)
+            rows.append({"op": name, "M": M, "N": 2304, "K": 768, "config": desc.format_config(sel.config),
+                         "level": sel.level, "us": round(ours * 1e3, 2), "torch": torch_name,
+                         "torch_us": round(t * 1e3, 2), "speedup": round(t / ours, 3),
+                         "tflops": round(2.0 * M * 2304 * 768 / ours / 1e9, 2)})
+            print(f"[ref-eval] {name} M={M}: {rows[-1]['us']} us ({rows[-1]['config']}, {sel.level}) vs "
+                  f"{torch_name} {rows[-1]['torch_us']} us", file=sys.stderr, flush=True)
+            del sets, runs
+        torch.cuda.empty_cache()
+    return rows
+
+
 def _shape_str(shape) -> str:
     if isinstance(shape, dict):
         if "OC" in shape:
@@ -699,6 +746,9 @@ def main():
                     help="launch a plain 1 GiB device copy 5 times (HBM counter calibration) and exit")
     ap.add_argument("--vs-libraries", action="store_true",
                     help="print this library's picks against the same ops composed from torch calls and exit")
+    ap.add_argument("--reference-eval", action="store_true",
+                    help="print the reference's own evaluation sweep (M = 1..126, N = 2304, K = 768, three ops) "
+                         "with the no-measurement select against torch, and exit")
     ap.add_argument("--probe-reads", action="store_true",
                     help="print the read bandwidth of the kernels' partition patterns (icpp_read_probe) and exit")
     args = ap.parse_args()
@@ -725,6 +775,9 @@ def main():
         return 0
     if args.vs_libraries:
         print(json.dumps({"vs_libraries": vs_libraries()}), flush=True)
+        return 0
+    if args.reference_eval:
+        print(json.dumps({"reference_eval": reference_eval()}), flush=True)
         return 0
     if args.op:  # one family of per-op rows only (profiling runs)
         print(json.dumps({"ops": bench_ops(args.quick, args.op, args.op_configs, args.row_index)}), flush=True)
