@@ -526,7 +526,10 @@ def _descriptors():
           gemm_bias_act.descriptor("silu", "bf16"), gemm_bias_act.descriptor("gelu_erf", "f16"),
           gemm_bias_layernorm.DESCRIPTOR, fp8_gemm_bias_act.DESCRIPTOR, conv2d.DESCRIPTOR] + \
         list(conv2d_fused.DESCRIPTORS.values())
-    return {d.name: d for d in ds}
+    out = {d.name: d for d in ds}
+    # a second dtype of a name is keyed name_dtype: ReLU in fp16, the reference's own gemm_bias_act
+    out["gemm_bias_relu_f16"] = gemm_bias_act.descriptor("relu", "f16")
+    return out
 
 
 def main(argv=None) -> int:  # pragma: no cover - device tool

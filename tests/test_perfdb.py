@@ -202,7 +202,7 @@ def test_sampling_plan_conv():
     assert all(conv2d.DESCRIPTOR.get_raw_configs(**p) for p in plan)
 
 
-SHIPPED = ["gemm_splitk_f16", "gemm_bias_gelu_tanh_bf16", "gemm_bias_relu_bf16", "gemm_bias_silu_bf16",
+SHIPPED = ["gemm_splitk_f16", "gemm_bias_gelu_tanh_bf16", "gemm_bias_relu_bf16", "gemm_bias_silu_bf16", "gemm_bias_relu_f16",
            "gemm_bias_layernorm_f16", "fp8_gemm_bias_silu_fp8",
            "conv2d_f16", "conv2d_relu_f16", "conv2d_bn_f16", "conv2d_bn_relu_f16", "conv_bn_add_relu_f16",
            "gemm_bias_gelu_erf_f16"]
