@@ -543,9 +543,10 @@ def vs_libraries():
 
 
 def reference_eval():
-    """The reference's own evaluation sweep (evaluation/gemm_three_ops_formula_summary.csv:
+    """The reference's own evaluation sweeps (evaluation/gemm_three_ops_formula_summary.csv:
     gemm, gemm_bias_act (ReLU), gemm_bias_layernorm at M = 1, 6, ..., 126, N = 2304,
-    K = 768, fp16 in): the config the reference's `build_kernel(config=None)` analogue
+    K = 768, fp16 in; conv2d_formula_changed_after_costmodel.csv: nine 3x3 fp16 NHWC
+    convolutions): the config the reference's `build_kernel(config=None)` analogue
     picks without measuring anything (`select_config`: table, residual or formula
     level), against the op composed from torch calls, both timed over the same
     rotated input copies (larger than the MALL)."""
@@ -585,6 +586,35 @@ def reference_eval():
             print(f"[ref-eval] {name} M={M}: {rows[-1]['us']} us ({rows[-1]['config']}, {sel.level}) vs "
                   f"{torch_name} {rows[-1]['torch_us']} us", file=sys.stderr, flush=True)
             del sets, runs
+        torch.cuda.empty_cache()
+    # the reference's conv evaluation (evaluation/conv2d_formula_changed_after_costmodel.csv: 3x3,
+    # stride 1, pad 1, fp16 NHWC, formula-selected config against torch's convolution)
+    from icpp_tuning_amd.kernels import conv2d as CV
+    desc, tuner = CV.DESCRIPTOR, AdaptiveTuner(CV.DESCRIPTOR)
+    for (Nb, C, H, F_out) in ((4, 64, 224, 64), (8, 64, 224, 64), (12, 64, 112, 64), (20, 64, 224, 64),
+                              (20, 512, 14, 512), (24, 256, 28, 512), (32, 64, 56, 192), (36, 512, 28, 512),
+                              (60, 64, 112, 64)):
+        shape = dict(N=Nb, C=C, H=H, W=H, OC=F_out, KH=3, KW=3, stride=1, padding=1)
+        sel = tuner.select(**shape)
+        sets = [desc.make_inputs(**shape)]
+        copies = max(1, min(16, -(-(600 << 20) // max(1, input_bytes(sets[0])))))
+        sets += [desc.make_inputs(**shape) for _ in range(copies - 1)]
+        runs = [desc.make_runner(sel.config, d, **shape) for d in sets]
+        reps = max(20, 2 * copies)
+        benchmark_ms(runs, warmup=copies, reps=reps)
+        ours = benchmark_ms(runs, warmup=copies, reps=reps)
+        views = [{"Xc": d["X"].permute(0, 3, 1, 2), "Wc": d["W"].permute(3, 0, 1, 2).contiguous().permute(0, 3, 1, 2)}
+                 for d in sets]
+        t = benchmark_ms([(lambda v=v: F.conv2d(v["Xc"], v["Wc"], padding=1)) for v in views], warmup=copies,
+                         reps=reps)
+        flops = 2.0 * Nb * H * H * F_out * C * 9
+        rows.append({"op": "conv2d", **shape, "config": desc.format_config(sel.config), "level": sel.level,
+                     "us": round(ours * 1e3, 2), "torch": "conv2d (MIOpen, channels-last)",
+                     "torch_us": round(t * 1e3, 2), "speedup": round(t / ours, 3),
+                     "tflops": round(flops / ours / 1e9, 1)})
+        print(f"[ref-eval] conv2d {shape}: {rows[-1]['us']} us ({rows[-1]['config']}, {sel.level}) vs "
+              f"{rows[-1]['torch']} {rows[-1]['torch_us']} us", file=sys.stderr, flush=True)
+        del sets, runs, views
         torch.cuda.empty_cache()
     return rows
 
