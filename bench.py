@@ -107,58 +107,6 @@ def sustained_clock(steps_fns, kernel_s: float, seconds: float = 0.25):
     return (ticks / rt * 100.0 if rt > 0 else None), rt / 1e8, s.elapsed_time(e) / 1e3 / n
 
 
-def probe_reads():
-    """Read bandwidth the memory system sustains for the partition patterns the kernels
-    use (icpp_read_probe): one 16 MiB matrix of 4096-byte rows read as 64 KiB row
-    blocks, as 128 / 64 / 16-byte column stripes (split-K and narrow-N layouts), by 16
-    workgroups only (the per-CU limit), and 256 MiB read in 1 MiB blocks.  Windows
-    rotate over 1.5 GiB so every launch reads HBM; HIP-event time per launch."""
-    import torch
-
-    from icpp_tuning_amd._lib import lib
-
-    total = 1536 << 20
-    buf = torch.ones(total // 4, dtype=torch.float32, device="cuda")
-    sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
-    stream = torch.cuda.current_stream().cuda_stream
-    rows = []
-    for (mib, ld, stripe, rpw, threads, passes, shared, what) in [
-            (16, 4096, 4096, 16, 1024, 1, 0, "64 KiB row blocks, 256 WGs"),
-            (16, 4096, 128, 512, 256, 1, 0, "128 B x 512-row stripes (split-K 8 over 32 column blocks), 256 WGs"),
-            (16, 4096, 64, 1024, 256, 1, 0, "64 B x 1024-row stripes, 256 WGs"),
-            (16, 4096, 16, 4096, 256, 1, 0, "16 B x 4096-row stripes (whole K per 16-column block), 256 WGs"),
-            (16, 4096, 4096, 256, 1024, 1, 0, "1 MiB row blocks, 16 WGs (per-CU HBM rate)"),
-            (16, 4096, 4096, 128, 1024, 1, 0, "512 KiB row blocks, 32 WGs"),
-            (16, 4096, 4096, 64, 1024, 1, 0, "256 KiB row blocks, 64 WGs"),
-            (256, 4096, 4096, 256, 1024, 1, 0, "1 MiB row blocks, 256 WGs"),
-            (16, 4096, 4096, 16, 1024, 16, 0, "64 KiB row blocks read 16 times (L2-resident after the first), 256 WGs"),
-            (16, 4096, 4096, 16, 1024, 16, 1, "one 64 KiB block read 16 times by all 256 WGs (shared hot lines)"),
-            (16, 4096, 4096, 16, 256, 16, 0, "64 KiB row blocks read 16 times, 256 threads per WG")]:
-        nbytes = mib << 20
-        windows = total // nbytes
-
-        def launch(i):
-            lib().call("icpp_read_probe", buf.data_ptr() + (i % windows) * nbytes, nbytes, ld, stripe, rpw, threads,
-                       passes, shared, sink.data_ptr(), sink.numel(), stream)
-        for i in range(3):
-            launch(i)
-        torch.cuda.synchronize()
-        reps = 24 if mib > 64 else 96
-        s, e = _events()
-        s.record()
-        for i in range(reps):
-            launch(i + 3)
-        e.record()
-        torch.cuda.synchronize()
-        us = s.elapsed_time(e) / reps * 1e3
-        moved = nbytes * passes  # bytes delivered to the CUs
-        rows.append({"pattern": what, "mib": mib, "passes": passes, "us": round(us, 2),
-                     "gbps": round(moved / us / 1e3, 1)})
-        print(f"[probe] {mib} MiB x {passes}, {what}: {us:.2f} us, {moved / us / 1e3:.0f} GB/s into the CUs",
-              file=sys.stderr, flush=True)
-    return rows
-
-
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -779,8 +727,6 @@ def main():
     ap.add_argument("--reference-eval", action="store_true",
                     help="print the reference's own evaluation sweep (M = 1..126, N = 2304, K = 768, three ops) "
                          "with the no-measurement select against torch, and exit")
-    ap.add_argument("--probe-reads", action="store_true",
-                    help="print the read bandwidth of the kernels' partition patterns (icpp_read_probe) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
@@ -799,9 +745,6 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes_read": src.numel() * 4, "calibrate_copy_bytes_written": dst.numel() * 4}))
-        return 0
-    if args.probe_reads:
-        print(json.dumps({"read_probe": probe_reads()}), flush=True)
         return 0
     if args.vs_libraries:
         print(json.dumps({"vs_libraries": vs_libraries()}), flush=True)

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libicpp_hip.so"
 RESOURCES_PATH = PKG / "libicpp_hip.resources.json"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 FAMILY = {"gemm": 0, "gemm_ln_stats": 1, "gemm_ln_row": 2, "conv2d": 3}
 FAMILY_NAME = {v: k for k, v in FAMILY.items()}
 DTYPE = {"f16": 0, "bf16": 1, "fp8": 2, "f32": 3}
@@ -31,7 +31,7 @@ EXPORTED_SYMBOLS = (
     "icpp_layernorm_fwd", "icpp_layernorm_bwd_workspace_bytes", "icpp_layernorm_bwd", "icpp_softmax",
     "icpp_softmax_scaled_masked",
     "icpp_gemm_bias_residual_layernorm", "icpp_qkv_split_heads", "icpp_merge_heads", "icpp_attention_fwd",
-    "icpp_clock_probe", "icpp_gemm_noalloc", "icpp_read_probe",
+    "icpp_clock_probe", "icpp_gemm_noalloc", "icpp_gemm_bias_layernorm_workspace_bytes",
 )
 CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
@@ -63,6 +63,7 @@ _SIGNATURES = {
     "icpp_num_instances": (_i, [_i]),
     "icpp_instance_info": (_i, [_i, _i, ctypes.POINTER(IcppTile)]),
     "icpp_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "icpp_gemm_bias_layernorm_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "icpp_gemm": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp, _sz, _vp]),
     "icpp_gemm_bias_layernorm": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz, _vp]),
     "icpp_gemm_bias_residual_layernorm": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _sz,
@@ -80,7 +81,6 @@ _SIGNATURES = {
     "icpp_merge_heads": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "icpp_clock_probe": (_i, [_vp, ctypes.c_double, _vp]),
     "icpp_gemm_noalloc": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp]),
-    "icpp_read_probe": (_i, [_vp, _sz, ctypes.c_uint, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
 }
 
 
@@ -117,6 +117,9 @@ class Lib:
 
     def workspace_bytes(self, family: int, inst: int, M: int, N: int, K: int, split_k: int) -> int:
         return int(self._dll.icpp_workspace_bytes(family, inst, M, N, K, split_k))
+
+    def ln_workspace_bytes(self, family: int, inst: int, M: int, N: int, K: int) -> int:
+        return int(self._dll.icpp_gemm_bias_layernorm_workspace_bytes(family, inst, M, N, K))
 
     def layernorm_bwd_workspace_bytes(self, dtype: int, M: int, N: int, ld: int) -> int:
         return int(self._dll.icpp_layernorm_bwd_workspace_bytes(dtype, M, N, ld))

@@ -99,6 +99,43 @@ KArgs base_args() {
   return a;
 }
 
+// Validate an icpp_gemm-style call and fill the kernel arguments (split-K planned,
+// no workspace attached).  `what` names the entry point in error messages.
+int gemm_prepare(const char* what, int inst, const void* A, const void* B, const void* bias, void* C, int M, int N,
+                 int K, int lda, int ldb, int ldc, int act, float scale_a, float scale_b, int split_k,
+                 const Instance** out_in, KArgs* out) {
+  const Instance* in = lookup(ICPP_FAMILY_GEMM, inst);
+  if (!in) return fail(ICPP_E_INSTANCE, "%s: no GEMM instance %d", what, inst);
+  const icpp_tile_t& t = in->tile;
+  if (!A || !B || !C) return fail(ICPP_E_ARG, "%s: null tensor", what);
+  if (M <= 0 || N <= 0 || K <= 0) return fail(ICPP_E_SHAPE, "%s: empty shape M=%d N=%d K=%d", what, M, N, K);
+  if (act < ICPP_ACT_NONE || act > ICPP_ACT_GELU_ERF) return fail(ICPP_E_ARG, "%s: bad act %d", what, act);
+  if (split_k < 1) return fail(ICPP_E_ARG, "%s: split_k=%d", what, split_k);
+  const int e = esz_of(t.dtype);
+  const int vec = 16 / e;
+  if (N % 8 || lda % vec || ldb % vec || ldc % 8 || lda < K || ldb < N || ldc < N)
+    return fail(ICPP_E_SHAPE, "%s: need N%%8==0, lda,ldb multiples of %d, ldc%%8==0 (N=%d lda=%d ldb=%d ldc=%d)",
+                what, vec, N, lda, ldb, ldc);
+  if (K % t.block_k || split_k > K / t.block_k)
+    return fail(ICPP_E_SHAPE, "%s: K=%d must be a multiple of block_k=%d with at least split_k=%d K tiles", what, K,
+                t.block_k, split_k);
+  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias)))
+    return fail(ICPP_E_ARG, "%s: pointers must be 16-byte aligned", what);
+  if ((uint64_t)t.block_m * lda * e > 0x7FFFFFFFull || (uint64_t)K * ldb * e > 0xFFFFFFF0ull ||
+      (uint64_t)t.block_m * ldc * 2 > 0x7FFFFFFFull)
+    return fail(ICPP_E_SHAPE, "%s: operand exceeds the buffer range (block rows of A / C < 2 GiB, B < 4 GiB)", what);
+  KArgs a = base_args();
+  a.A = A; a.B = B; a.bias = bias; a.C = C;
+  a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+  a.act = act; a.alpha = scale_a * scale_b;
+  a.splits = plan_splits(K / t.block_k, t.block_k, split_k, &a.k_split);
+  a.tiles_m = ceil_div(M, t.block_m);
+  a.tiles_n = ceil_div(N, t.block_n);
+  *out_in = in;
+  *out = a;
+  return ICPP_OK;
+}
+
 }  // namespace
 
 int register_instance(const Instance& inst) {
@@ -110,8 +147,8 @@ int register_instance(const Instance& inst) {
 
 // The row-op translation unit (icpp_rowops.hip) reports through the same buffer.
 int set_last_error(int code, const char* msg) { return fail(code, "%s", msg); }
-int layernorm_rows_f16(const void* X, const void* R, const void* W, const void* B, void* Y, int M, int N, float eps,
-                       hipStream_t s);  // icpp_rowops.hip
+int layernorm_rows_f16(const void* X, const void* R, const float* block_mean, int bm_cols, int bm_width, const void* W,
+                       const void* B, void* Y, int M, int N, float eps, hipStream_t s);  // icpp_rowops.hip
 
 }  // namespace icpp
 
@@ -154,33 +191,12 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
               int M, int N, int K, int lda, int ldb, int ldc, int act,
               float scale_a, float scale_b, int split_k,
               void* workspace, size_t ws_bytes, void* stream) {
-  const Instance* in = lookup(ICPP_FAMILY_GEMM, inst);
-  if (!in) return fail(ICPP_E_INSTANCE, "icpp_gemm: no GEMM instance %d", inst);
+  const Instance* in = nullptr;
+  KArgs a;
+  if (int rc = gemm_prepare("icpp_gemm", inst, A, B, bias, C, M, N, K, lda, ldb, ldc, act, scale_a, scale_b, split_k,
+                            &in, &a))
+    return rc;
   const icpp_tile_t& t = in->tile;
-  if (!A || !B || !C) return fail(ICPP_E_ARG, "icpp_gemm: null tensor");
-  if (M <= 0 || N <= 0 || K <= 0) return fail(ICPP_E_SHAPE, "icpp_gemm: empty shape M=%d N=%d K=%d", M, N, K);
-  if (act < ICPP_ACT_NONE || act > ICPP_ACT_GELU_ERF) return fail(ICPP_E_ARG, "icpp_gemm: bad act %d", act);
-  if (split_k < 1) return fail(ICPP_E_ARG, "icpp_gemm: split_k=%d", split_k);
-  const int e = esz_of(t.dtype);
-  const int vec = 16 / e;
-  if (N % 8 || lda % vec || ldb % vec || ldc % 8 || lda < K || ldb < N || ldc < N)
-    return fail(ICPP_E_SHAPE, "icpp_gemm: need N%%8==0, lda,ldb multiples of %d, ldc%%8==0 (N=%d lda=%d ldb=%d ldc=%d)",
-                vec, N, lda, ldb, ldc);
-  if (K % t.block_k || split_k > K / t.block_k)
-    return fail(ICPP_E_SHAPE, "icpp_gemm: K=%d must be a multiple of block_k=%d with at least split_k=%d K tiles", K,
-                t.block_k, split_k);
-  if (!aligned16(A) || !aligned16(B) || !aligned16(C) || (bias && !aligned16(bias)))
-    return fail(ICPP_E_ARG, "icpp_gemm: pointers must be 16-byte aligned");
-  if ((uint64_t)t.block_m * lda * e > 0x7FFFFFFFull || (uint64_t)K * ldb * e > 0xFFFFFFF0ull ||
-      (uint64_t)t.block_m * ldc * 2 > 0x7FFFFFFFull)
-    return fail(ICPP_E_SHAPE, "icpp_gemm: operand exceeds the buffer range (block rows of A / C < 2 GiB, B < 4 GiB)");
-  KArgs a = base_args();
-  a.A = A; a.B = B; a.bias = bias; a.C = C;
-  a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
-  a.act = act; a.alpha = scale_a * scale_b;
-  a.splits = plan_splits(K / t.block_k, t.block_k, split_k, &a.k_split);
-  a.tiles_m = ceil_div(M, t.block_m);
-  a.tiles_n = ceil_div(N, t.block_n);
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(a.tiles_m * a.tiles_n * a.splits);  // one workgroup per (tile, K split) item
   if (a.splits > 1) {
@@ -195,6 +211,18 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
     return check_launch(launch_splitk_reduce(t.dtype, a.ws, C, bias, M, N, ldc, a.splits, a.alpha, act, s), "splitk_reduce");
   }
   return check_launch(in->launch(a, grid, s), t.name);
+}
+
+size_t icpp_gemm_bias_layernorm_workspace_bytes(int family, int inst, int M, int N, int K) {
+  (void)K;
+  if (M <= 0 || N <= 0) return 0;
+  if (family == ICPP_FAMILY_GEMM) {
+    const Instance* in = lookup(ICPP_FAMILY_GEMM, inst);
+    if (!in) return 0;
+    return (size_t)M * ceil_div(N, in->wave_tile_n) * sizeof(float);
+  }
+  if (family == ICPP_FAMILY_GEMM_LN_STATS) return icpp_workspace_bytes(family, inst, M, N, K, 1);
+  return 0;
 }
 
 int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
@@ -227,9 +255,21 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
       if (r0 < y0 + bytes && y0 < r0 + bytes)
         return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: the GEMM family needs a residual that does not overlap Y");
     }
-    int rc = icpp_gemm(inst, A, B, bias, Y, M, N, K, K, N, N, ICPP_ACT_NONE, 1.f, 1.f, 1, workspace, ws_bytes, stream);
+    // The GEMM stores Y centred on per-(row, wave column block) means and writes the
+    // means (fp32) into the workspace; the row LayerNorm adds them back.
+    KArgs a;
+    if (int rc = gemm_prepare("icpp_gemm_bias_layernorm", inst, A, B, bias, Y, M, N, K, K, N, N, ICPP_ACT_NONE, 1.f,
+                              1.f, 1, &gi, &a))
+      return rc;
+    a.stat_cols = ceil_div(N, gi->wave_tile_n);
+    const size_t need = (size_t)M * a.stat_cols * sizeof(float);
+    if (!workspace || ws_bytes < need || !aligned16(workspace))
+      return fail(ICPP_E_WORKSPACE, "icpp_gemm_bias_layernorm: needs %zu workspace bytes (got %zu)", need, ws_bytes);
+    a.ws = (float*)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    int rc = check_launch(gi->launch(a, dim3(a.tiles_m * a.tiles_n), s), gi->tile.name);
     if (rc) return rc;
-    return layernorm_rows_f16(Y, residual, gamma, beta, Y, M, N, eps, (hipStream_t)stream);
+    return layernorm_rows_f16(Y, residual, a.ws, a.stat_cols, gi->wave_tile_n, gamma, beta, Y, M, N, eps, s);
   }
   if (family != ICPP_FAMILY_GEMM_LN_ROW && family != ICPP_FAMILY_GEMM_LN_STATS)
     return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: family %d is not a LayerNorm family", family);

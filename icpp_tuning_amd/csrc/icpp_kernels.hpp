@@ -1024,6 +1024,16 @@ gemm_kernel(KArgs p) {
                         [&](int tm, int tn, int g, f32x4) ICPP_INLINE { return value4(tm, tn, g); });
     };
 
+    // a row's sum over this wave's columns, reduced across the lanes sharing the row
+    auto lane_reduce = [&](float v) ICPP_INLINE {
+      if (MF == 16) {
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+      } else {
+        v += __shfl_xor(v, 32);
+      }
+      return v;
+    };
     if constexpr (EPI == EPI_STORE) {
       if (p.partial) {
         float* ws = p.ws + (size_t)kz * p.M * p.N;
@@ -1066,11 +1076,41 @@ gemm_kernel(KArgs p) {
             const int n = out_col(tn, g);
             bv[tn][g] = (bias != nullptr && n < p.N) ? Vec4Store<BiasT>::ld(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
           }
+        // LayerNorm producer (p.stat_cols > 0, act none): each row's values over this
+        // wave's WTN columns are stored minus their mean, and the mean goes to
+        // ws[m * stat_cols + column block] in fp32.  The LayerNorm pass adds it back,
+        // so the 16-bit copy carries only the spread around the block mean: a row whose
+        // mean is far from zero keeps the fp32 precision the reference's X has.
+        float bmean[G::TM];
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) bmean[tm] = 0.f;
+        if (p.stat_cols > 0) {
+          const int wcol0 = col0 + wn * G::WTN;
+          const int wcnt = max(0, min(G::WTN, p.N - wcol0));
+          const int scol = wcol0 / G::WTN;
+#pragma unroll
+          for (int tm = 0; tm < G::TM; ++tm) {
+            float s = 0.f;
+#pragma unroll
+            for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+              for (int g = 0; g < NG; ++g) {
+                const f32x4 v = get4(tm, tn, g);
+                if (out_col(tn, g) < p.N)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) s += v[e] * p.alpha + bv[tn][g][e];
+              }
+            s = lane_reduce(s);
+            bmean[tm] = wcnt > 0 ? s / (float)wcnt : 0.f;
+            const int m = out_row(tm);
+            if (lane < MF && m < p.M && scol < p.stat_cols) p.ws[(size_t)m * p.stat_cols + scol] = bmean[tm];
+          }
+        }
         dispatch_act(p.act, [&](auto ACT) ICPP_INLINE {
           store_staged([&](int tm, int tn, int g) ICPP_INLINE {
             f32x4 v = get4(tm, tn, g);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = act_fn<decltype(ACT)::value>(v[e] * p.alpha + bv[tn][g][e]);
+            for (int e = 0; e < 4; ++e) v[e] = act_fn<decltype(ACT)::value>(v[e] * p.alpha + bv[tn][g][e]) - bmean[tm];
             return v;
           });
         });
@@ -1114,16 +1154,6 @@ gemm_kernel(KArgs p) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // row sums over this wave's columns, reduced across the lanes sharing a row
-      auto lane_reduce = [&](float v) ICPP_INLINE {
-        if (MF == 16) {
-          v += __shfl_xor(v, 16);
-          v += __shfl_xor(v, 32);
-        } else {
-          v += __shfl_xor(v, 32);
-        }
-        return v;
-      };
       const int wcol0 = col0 + wn * G::WTN;
       const int wcnt = max(0, min(G::WTN, p.N - wcol0));
       if constexpr (EPI == EPI_LN_STATS) {
@@ -1156,12 +1186,15 @@ gemm_kernel(KArgs p) {
             ws[((size_t)m * p.stat_cols + scol) * 2 + 0] = mean;
             ws[((size_t)m * p.stat_cols + scol) * 2 + 1] = q;
           }
+          // X is stored centred on the block mean (the finalize adds it back), so the
+          // 16-bit copy keeps the precision of the fp32 values whatever the row's offset
 #pragma unroll
           for (int tn = 0; tn < G::TN; ++tn)
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
               const int n = out_col(tn, g);
-              f32x4 v = {xs[tm][tn][4 * g], xs[tm][tn][4 * g + 1], xs[tm][tn][4 * g + 2], xs[tm][tn][4 * g + 3]};
+              f32x4 v = {xs[tm][tn][4 * g] - mean, xs[tm][tn][4 * g + 1] - mean, xs[tm][tn][4 * g + 2] - mean,
+                         xs[tm][tn][4 * g + 3] - mean};
               if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
             }
         }
@@ -1443,8 +1476,10 @@ splitk_reduce_kernel(const float* __restrict__ ws, void* C, const void* bias, in
 
 // ---------------------------------------------------------------------------
 // Two-pass LayerNorm finalize: combine per-(row, column block) (mean, M2)
-// partials (Chan et al. pairwise update), then normalise the row in place.
-// One wave per row; 4 rows per 256-thread workgroup.
+// partials (Chan et al. pairwise update), then normalise the row in place.  The
+// GEMM stored each block centred on its own mean, so x = stored + (block mean -
+// row mean) relative to the row mean.  One wave per row; 4 rows per 256-thread
+// workgroup.
 // ---------------------------------------------------------------------------
 template <int DT>
 __global__ void __launch_bounds__(256)
@@ -1476,8 +1511,10 @@ ln_finalize_kernel(void* C, const float* __restrict__ stats, const void* gamma, 
     f32x4 x = Vec4Store<OutT>::ld(row + n);
     const f32x4 gv = Vec4Store<BiasT>::ld(g + n);
     const f32x4 bv = Vec4Store<BiasT>::ld(b + n);
+    // block_cols is a multiple of 4, so the 4 columns share one block
+    const float d = stats[((size_t)m * stat_cols + n / block_cols) * 2 + 0] - mean;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = (x[e] - mean) * rstd * gv[e] + bv[e];
+    for (int e = 0; e < 4; ++e) x[e] = (x[e] + d) * rstd * gv[e] + bv[e];
     Vec4Store<OutT>::st(row + n, x);
   }
 }

@@ -125,13 +125,16 @@ __device__ __forceinline__ void row_reduce2(float& a, float& b, int tpr, float (
 // LayerNorm forward: y = (x - mean) * rstd * w + b, mean / rstd (fp32) per row
 // (reference _layer_norm_fwd_fused: centred two-pass variance, rstd = 1/sqrt(var+eps)).
 // ---------------------------------------------------------------------------
-// With a residual R (may be null), x = X + R (R has X's row stride).  Y may be X:
-// every row is held in registers before any of it is written.
+// With a residual R (may be null), x = X + R (R has X's row stride).  With block
+// means BMN (may be null; [M][bm_cols] fp32, block j covering columns
+// j*bm_width .. +bm_width-1, bm_width a multiple of VEC) x also gains its block's
+// mean: X then holds values stored centred on those means by the producing GEMM.
+// Y may be X: every row is held in registers before any of it is written.
 template <typename T, int VEC, int CPT>
 __global__ void __launch_bounds__(1024)
-layernorm_fwd_kernel(const T* X, const T* R, const T* __restrict__ W, const T* __restrict__ B, T* Y,
-                     float* __restrict__ mean_out, float* __restrict__ rstd_out, int M, int N, int ldx, int ldy,
-                     float eps, int tpr) {
+layernorm_fwd_kernel(const T* X, const T* R, const float* __restrict__ BMN, const T* __restrict__ W,
+                     const T* __restrict__ B, T* Y, float* __restrict__ mean_out, float* __restrict__ rstd_out, int M,
+                     int N, int ldx, int ldy, float eps, int tpr, int bm_cols, int bm_width) {
   __shared__ float red[2][MAX_WAVES];
   int slot = 0;
   const int rpb = blockDim.x / tpr;
@@ -151,6 +154,11 @@ layernorm_fwd_kernel(const T* X, const T* R, const T* __restrict__ W, const T* _
         load_chunk<T, VEC>(R + (size_t)row * ldx + (size_t)c * VEC, r);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) x[i][e] += r[e];
+      }
+      if (BMN != nullptr) {
+        const float bm = BMN[(size_t)row * bm_cols + (c * VEC) / bm_width];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) x[i][e] += bm;
       }
     } else {
 #pragma unroll
@@ -701,18 +709,20 @@ hipError_t dispatch_cpt(const RowGeom& g, F&& launch) {
 
 template <typename T>
 int ln_fwd_t(const void* X, const void* R, const void* W, const void* B, void* Y, float* mean, float* rstd, int M,
-             int N, int ldx, int ldy, float eps, hipStream_t s) {
+             int N, int ldx, int ldy, float eps, hipStream_t s, const float* bmn = nullptr, int bm_cols = 0,
+             int bm_width = 1) {
   constexpr int V = 16 / (int)sizeof(T);
   const bool vec_ok = N % V == 0 && ldx % V == 0 && ldy % V == 0 && aligned16(X) && aligned16(Y) &&
-                      aligned16(W) && aligned16(B) && (R == nullptr || aligned16(R));
+                      aligned16(W) && aligned16(B) && (R == nullptr || aligned16(R)) &&
+                      (bmn == nullptr || bm_width % V == 0);
   RowGeom g;
   if (!row_geom(N, vec_ok ? V : 1, vec_ok ? 8 : 16, &g)) return set_error(ICPP_E_SHAPE, "icpp_layernorm_fwd: N too large");
   const int rpb = g.block / g.tpr;
   const dim3 grid((M + rpb - 1) / rpb);
   hipError_t e = dispatch_cpt<T>(g, [&](auto VEC, auto CPT) {
     hipLaunchKernelGGL((layernorm_fwd_kernel<T, decltype(VEC)::value, decltype(CPT)::value>), grid, dim3(g.block), 0, s,
-                       (const T*)X, (const T*)R, (const T*)W, (const T*)B, (T*)Y, mean, rstd, M, N, ldx, ldy, eps,
-                       g.tpr);
+                       (const T*)X, (const T*)R, bmn, (const T*)W, (const T*)B, (T*)Y, mean, rstd, M, N, ldx, ldy,
+                       eps, g.tpr, bm_cols, bm_width);
     return hipGetLastError();
   });
   return e == hipSuccess ? ICPP_OK : set_error((int)e, hipGetErrorString(e));
@@ -797,11 +807,13 @@ int check_rows(const char* fn, int dtype, int M, int N, int ld_in, int ld_out) {
 }  // namespace
 
 namespace icpp {
-// Y = LayerNorm(X [+ R]) * W + B over rows of an f16 [M, N] tensor (row stride N),
-// Y may be X; for icpp_gemm_bias_residual_layernorm's GEMM-then-LayerNorm strategy.
-int layernorm_rows_f16(const void* X, const void* R, const void* W, const void* B, void* Y, int M, int N, float eps,
-                       hipStream_t s) {
-  return ln_fwd_t<_Float16>(X, R, W, B, Y, nullptr, nullptr, M, N, N, N, eps, s);
+// Y = LayerNorm(X [+ R] + block_mean) * W + B over rows of an f16 [M, N] tensor (row
+// stride N), Y may be X; for icpp_gemm_bias_residual_layernorm's GEMM-then-LayerNorm
+// strategy, whose GEMM stores X centred on per-(row, bm_width-column block) means
+// block_mean [M][bm_cols] (null: X is stored as is).
+int layernorm_rows_f16(const void* X, const void* R, const float* block_mean, int bm_cols, int bm_width, const void* W,
+                       const void* B, void* Y, int M, int N, float eps, hipStream_t s) {
+  return ln_fwd_t<_Float16>(X, R, W, B, Y, nullptr, nullptr, M, N, N, N, eps, s, block_mean, bm_cols, bm_width);
 }
 }  // namespace icpp
 

@@ -62,6 +62,29 @@ def config3(M=8192, N=1024, K=4096, device="cpu"):
     return {k: v.to(device) for k, v in d.items()}
 
 
+C3_OFFSETS = ("bias+64", "bias+256", "row_mean")
+
+
+def config3_offset(M=8192, N=1024, K=4096, kind="bias+256", device="cpu"):
+    """Config-3 inputs whose pre-LayerNorm X = A.B + bias sits far from zero relative
+    to its spread (row std ~1): "bias+64" / "bias+256" add a column offset common to
+    every row; "row_mean" gives each row its own mean in [100, 400] (A[:, 0] ~
+    U(100, 400), B[0, :] = 1).  This is the regime where the reference's fp32 X
+    (gemm_bias_layernorm.py:59, :66, :103) differs from a 16-bit copy of X."""
+    d = config3(M, N, K)
+    if kind == "bias+64":
+        d["bias"] = (d["bias"].float() + 64.0).to(torch.float16)
+    elif kind == "bias+256":
+        d["bias"] = (d["bias"].float() + 256.0).to(torch.float16)
+    elif kind == "row_mean":
+        g = torch.Generator().manual_seed(3100)
+        d["A"][:, 0] = (torch.rand(M, generator=g) * 300.0 + 100.0).to(torch.float16)
+        d["B"][0, :] = 1.0
+    else:
+        raise ValueError(f"unknown offset kind {kind!r} (one of {C3_OFFSETS})")
+    return {k: v.to(device) for k, v in d.items()}
+
+
 def config4(N=32, H=56, W=56, C=64, F=64, KH=3, KW=3, device="cpu"):
     X = normal((N, H, W, C), 1.0, 4000 + 0).to(torch.float16)
     Wt = normal((KH, KW, C, F), 1.0 / math.sqrt(KH * KW * C), 4000 + 1).to(torch.float16)
@@ -91,4 +114,5 @@ def config5(M=256, N=4096, K=4096, device="cpu"):
     return {"A": aq.to(device), "B": bq.to(device), "scale_a": sa, "scale_b": sb, "bias": bias.to(device)}
 
 
-__all__ = ["config1", "config2", "config3", "config4", "config5", "gemm_inputs", "normal", "quantize_e4m3"]
+__all__ = ["C3_OFFSETS", "config1", "config2", "config3", "config3_offset", "config4", "config5", "gemm_inputs",
+           "normal", "quantize_e4m3"]

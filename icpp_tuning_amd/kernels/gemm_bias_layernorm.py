@@ -10,12 +10,18 @@ chosen per shape by the tuner:
   "row"       (gemm_ln_row)    one workgroup owns whole rows (N <= block_N):
               mean and centred variance reduced in registers + LDS, no
               intermediate in HBM, one launch.
-  "two_pass"  (gemm_ln_stats)  GEMM tiles write X (f16) into Y and a per-(row,
+  "two_pass"  (gemm_ln_stats)  GEMM tiles write X into Y and a per-(row,
               wave column block) (mean, M2) pair into the workspace; a finalize
               pass merges the pairs (Chan et al.) and normalises Y in place.
-  "gemm_ln"   (gemm, f16)      a plain GEMM + bias into Y (any GEMM tile, staged
-              stores), then the row LayerNorm kernel in place: the same HBM
-              traffic as two-pass, without the statistics epilogue.
+  "gemm_ln"   (gemm, f16)      a GEMM + bias into Y (any GEMM tile, staged
+              stores) plus per-(row, wave column block) means in the workspace,
+              then the row LayerNorm kernel in place: the same HBM traffic as
+              two-pass, with only a mean in the epilogue.
+
+Both two-launch strategies keep X in Y as f16 values centred on their block's
+mean (the mean itself in fp32 in the workspace), where the reference keeps X in
+fp32 (:59, :66, :103): the 16-bit copy rounds only the spread around the block
+mean, so rows with a large common offset keep the fp32 precision.
 """
 
 from __future__ import annotations
@@ -123,7 +129,7 @@ class CompiledGemmLayerNorm:
     def __call__(self, A, B, bias, gamma, beta, out=None, residual=None):
         """``LayerNorm(A @ B + bias [+ residual]) * gamma + beta``; the residual ([M, N] f16, may be
         ``out``) is the add of the BERT attention-output / FFN-output blocks (end2end.py:76-79)."""
-        need = runtime.workspace_bytes(self.family, self.inst, self.M, self.N, self.K)
+        need = runtime.ln_workspace_bytes(self.family, self.inst, self.M, self.N, self.K)
         if need and (self._ws is None or self._ws.device != A.device):
             self._ws = runtime.alloc_workspace(need, A.device)
         if self.family == "gemm" and residual is not None and out is not None and _overlap(out, residual):

@@ -46,6 +46,11 @@ def workspace_bytes(family: str, inst: int, M: int, N: int, K: int, split_k: int
     return lib().workspace_bytes(FAMILY[family], inst, M, N, K, split_k)
 
 
+def ln_workspace_bytes(family: str, inst: int, M: int, N: int, K: int) -> int:
+    """Workspace of a GEMM+bias+LayerNorm call (icpp_gemm_bias_layernorm_workspace_bytes)."""
+    return lib().ln_workspace_bytes(FAMILY[family], inst, M, N, K)
+
+
 def alloc_workspace(nbytes: int, device) -> Optional[torch.Tensor]:
     if nbytes <= 0:
         return None
@@ -92,7 +97,7 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
     if out is None:
         out = torch.empty((M, N), dtype=h, device=a.device)
     py = _check(out, "out", h, (M, N), device=a.device)
-    need = workspace_bytes(family, inst, M, N, K, 1)
+    need = ln_workspace_bytes(family, inst, M, N, K)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = alloc_workspace(need, a.device)
     pws = workspace.data_ptr() if (need and workspace is not None) else None
@@ -310,4 +315,4 @@ def merge_heads(ctx: torch.Tensor, batch: int) -> torch.Tensor:
 
 __all__ = ["BIAS_DTYPE", "HEAD_DIM", "OUT_DTYPE", "ROW_DTYPE", "TORCH_DTYPE", "alloc_workspace", "conv2d_nhwc", "gemm",
            "attention_fwd", "gemm_bias_layernorm", "layernorm_bwd", "layernorm_fwd", "merge_heads", "qkv_split_heads", "softmax",
-           "softmax_scaled_masked", "workspace_bytes"]
+           "softmax_scaled_masked", "ln_workspace_bytes", "workspace_bytes"]

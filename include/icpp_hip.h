@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define ICPP_ABI_VERSION 1
+#define ICPP_ABI_VERSION 2
 
 /* instance families */
 enum icpp_family {
@@ -94,6 +94,10 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
  * strategy: ICPP_FAMILY_GEMM_LN_ROW (whole row per workgroup, N <= block_n,
  * no workspace) or ICPP_FAMILY_GEMM_LN_STATS (GEMM writes X into Y plus
  * per-block (mean, M2) into the workspace, then a finalize pass normalises Y).
+ * The reference keeps X in fp32 between its two kernels (:59, :66, :103); the
+ * two-launch strategies here keep X in Y as f16 values centred on the mean of
+ * their (row, wave column block), with that mean in fp32 in the workspace, so a
+ * row offset far above the row's spread loses no precision.
  */
 int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
                              const void* gamma, const void* beta, void* Y,
@@ -106,15 +110,25 @@ int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B,
  * (evaluation/end2end.py:76-79, :84-87: matmul + bias, + residual, F.layer_norm).
  * residual is [M, N] f16 (may be Y itself: each element is read before it is
  * written, by the same lane); null gives icpp_gemm_bias_layernorm.
- * family may also be ICPP_FAMILY_GEMM (an f16 GEMM instance): a plain GEMM + bias
- * into Y, then the row LayerNorm in place -- the same HBM traffic as the two-pass
- * family, any GEMM tile.  With that family the residual must not overlap Y
- * (ICPP_E_ARG otherwise): the GEMM writes Y before the LayerNorm reads it.
+ * family may also be ICPP_FAMILY_GEMM (an f16 GEMM instance): a GEMM + bias into
+ * Y (stored centred on per-(row, wave column block) means, the means in the
+ * workspace), then the row LayerNorm in place -- the same HBM traffic as the
+ * two-pass family, any GEMM tile.  With that family the residual must not overlap
+ * Y (ICPP_E_ARG otherwise): the GEMM writes Y before the LayerNorm reads it.
  */
 int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
                                       const void* residual, const void* gamma, const void* beta, void* Y,
                                       int M, int N, int K, float eps,
                                       void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Workspace bytes icpp_gemm_bias_layernorm / icpp_gemm_bias_residual_layernorm need
+ * for `family` (ICPP_FAMILY_GEMM_LN_ROW, _LN_STATS or ICPP_FAMILY_GEMM) and instance
+ * (0 when none).  It holds what the reference keeps in its fp32 X intermediate
+ * (gemm_bias_layernorm.py:175-186 allocates it per call): per-(row, column block)
+ * statistics, M * ceil(N / wave tile columns) * 4 or * 8 bytes.
+ */
+size_t icpp_gemm_bias_layernorm_workspace_bytes(int family, int inst, int M, int N, int K);
 
 /*
  * Y[N,OH,OW,F] = conv2d(X[N,H,W,C], W[KH,KW,C,F]), f16, fp32 accumulate.
@@ -261,21 +275,6 @@ int icpp_gemm_noalloc(int inst, const void* A, const void* B, const void* bias, 
  * held under that load.  seconds in (0, 10].
  */
 int icpp_clock_probe(unsigned long long* out, double seconds, void* stream);
-
-/*
- * Measurement aid, no counterpart in the reference: the read-bandwidth probe.  Reads
- * `bytes` of device memory viewed as rows of `ld` bytes, one workgroup of `threads`
- * (256 / 512 / 1024, a multiple of stripe / 16) per stripe of `stripe` bytes x
- * `rows_per_wg` rows, 16 bytes per
- * lane per load, 8 loads in flight per lane; neighbouring stripes share an XCD.
- * Each workgroup reads its stripe `passes` times (1-64; later passes hit L2), and
- * with `shared` non-zero every workgroup reads stripe 0 (the same lines).  Time it
- * with events to get the bandwidth a partition pattern sustains (the workgroup
- * count is (ld / stripe) * (bytes / ld / rows_per_wg) <= sink_ints; sink is a device
- * int array that is written only in a sentinel case).
- */
-int icpp_read_probe(const void* base, size_t bytes, unsigned ld, int stripe, int rows_per_wg, int threads,
-                    int passes, int shared, int* sink, size_t sink_ints, void* stream);
 
 #ifdef __cplusplus
 }

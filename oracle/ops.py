@@ -215,11 +215,3 @@ def fp8_gemm_bias_act_ref(Aq, Bq, scale_a: float, scale_b: float, bias, act: str
     if bias is not None:
         x = x + bias.float().cpu().unsqueeze(0)
     return apply_act(x, act)
-
-
-def op_flops(op: str, **s) -> float:
-    """Algorithmic mainloop FLOPs (reference gemm_bias_act.py:139, conv2d.py:71-72)."""
-    if op == "conv2d":
-        OH, OW = conv_out_hw(s["H"], s["W"], s["KH"], s["KW"], s.get("S", 1), s.get("P", 1))
-        return 2.0 * s["N"] * OH * OW * s["F"] * s["C"] * s["KH"] * s["KW"]
-    return 2.0 * s["M"] * s["N"] * s["K"]

@@ -160,6 +160,67 @@ def test_config3_gemm_bias_layernorm(gpu, N):
     _close(y, ref, 2e-2, 2e-2, f"config3 N={N} {k.config}")
 
 
+C3_OFFSETS = I.C3_OFFSETS
+
+
+@pytest.mark.parametrize("kind", C3_OFFSETS)
+@pytest.mark.parametrize("strategy", ["row", "two_pass", "gemm_ln"])
+def test_every_ln_instance_offset_rows(gpu, strategy, kind):
+    """Every instance of each LayerNorm strategy on rows far from zero (ragged M and N;
+    N = the row tile's width for whole-row instances)."""
+    M, K = 333, 512
+    fam = ln_mod.STRATEGY_FAMILY[strategy]
+    refs = {}
+    for inst in family_instances(fam):
+        if inst.dtype != "f16" or K % inst.bk:
+            continue
+        N = inst.bn if strategy == "row" else 776
+        if N not in refs:
+            d = I.config3_offset(M, N, K, kind)
+            refs[N] = (d, O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"]))
+        d, ref = refs[N]
+        raw = raw_from_inst(inst)
+        raw["strategy"] = strategy
+        print(f"[parity] {inst.name} {strategy} {kind} M={M} N={N} K={K}", flush=True)
+        k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+        y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
+        torch.cuda.synchronize()
+        _close(y, ref, 2e-2, 2e-2, f"{inst.name} {strategy} {kind}")
+
+
+@pytest.mark.parametrize("kind", C3_OFFSETS)
+@pytest.mark.parametrize("N", [768, 1024, 4096])
+def test_config3_offset_rows_every_strategy(gpu, N, kind):
+    """Full config-3 size (M = 8192, K = 4096) on rows far from zero: the tuner's pick and
+    the formula's best config of each strategy that serves N."""
+    from icpp_tuning_amd.autotuner.interface import rank_all
+
+    M, K = 8192, 4096
+    d = I.config3_offset(M, N, K, kind)
+    ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+    dev = {t: d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")}
+    configs, seen = [], set()
+    ranked = rank_all(ln_mod.DESCRIPTOR, M=M, N=N, K=K)
+    for strategy in ("row", "two_pass", "gemm_ln"):
+        top = next((e["raw_config"] for e in ranked if e["raw_config"].get("strategy") == strategy), None)
+        if top is not None:
+            configs.append(top)
+    configs.append(ln_mod.build_fused_kernel(M, N, K).config)
+    ran = 0
+    for raw in configs:
+        name = ln_mod.DESCRIPTOR.format_config(raw)
+        if name in seen:
+            continue
+        seen.add(name)
+        print(f"[parity] config3 offset {kind} N={N} {name}", flush=True)
+        k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+        y = k(dev["A"], dev["B"], dev["bias"], dev["gamma"], dev["beta"])
+        torch.cuda.synchronize()
+        _close(y, ref, 2e-2, 2e-2, f"config3 offset {kind} N={N} {name}")
+        ran += 1
+    assert ran >= (3 if N <= 1024 else 2)
+
+
 def test_every_conv_instance(gpu):
     Nb, H, W, C, F = 2, 9, 7, 64, 64
     d = I.config4(Nb, H, W, C, F)

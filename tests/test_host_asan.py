@@ -102,9 +102,6 @@ DRIVER = textwrap.dedent(r"""
     must_fail("icpp_clock_probe null", clk(None, 0.1, None))
     buf = (ctypes.c_ulonglong * 2)()
     must_fail("icpp_clock_probe seconds", clk(buf, 100.0, None))
-    rp = fn("icpp_read_probe", i, vp, sz, ctypes.c_uint, i, i, i, i, i, vp, sz, vp)
-    must_fail("icpp_read_probe stripe", rp(P, 1 << 20, 4096, 24, 8, 256, 1, 0, P, 1024, None))
-    must_fail("icpp_read_probe sink", rp(P, 1 << 20, 4096, 128, 8, 256, 1, 0, P, 1, None))
     if bad:
         print("\n".join(bad))
         sys.exit(3)

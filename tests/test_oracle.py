@@ -431,3 +431,38 @@ def test_attention_ref_matches_fp64_sdpa_and_loops():
                 for t in range(d):
                     o = sum(e[j] / tot * V[bh, j, t] for j in range(s))
                     assert abs(float(got[bi, i, hi * d + t]) - o) < 1e-5
+
+
+def _offset_regime(d):
+    """min over rows of |row mean| / row std of the fp32 X = A.B + bias the inputs give."""
+    x = O.gemm_bias_act_ref(d["A"], d["B"], d["bias"], "none")
+    return float((x.mean(dim=1).abs() / x.std(dim=1)).min())
+
+
+def test_config3_offset_inputs_are_in_the_regime():
+    """The LayerNorm offset cases really put X's rows far from zero -- mean >= 50 x std
+    for bias + 64, >= 100 x std for bias + 256 and the per-row means -- while the plain
+    config-3 draw stays near zero, and the oracle's output on them is still a unit-scale
+    LayerNorm (what an f16 copy of X cannot resolve: ulp 0.25 at 256)."""
+    from icpp_tuning_amd import inputs as I
+
+    M, N, K = 64, 256, 512
+    assert _offset_regime(I.config3_offset(M, N, K, "bias+64")) >= 50
+    assert _offset_regime(I.config3_offset(M, N, K, "bias+256")) >= 100
+    assert _offset_regime(I.config3_offset(M, N, K, "row_mean")) >= 100
+    plain = I.config3(M, N, K)
+    x = O.gemm_bias_act_ref(plain["A"], plain["B"], plain["bias"], "none")
+    assert float(x.mean(dim=1).abs().max()) < 1.0
+    d = I.config3_offset(M, N, K, "bias+256")
+    y = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+    z = (y - d["beta"].float()) / d["gamma"].float()
+    assert torch.allclose(z.mean(dim=1), torch.zeros(M), atol=1e-3)
+    assert torch.allclose(z.std(dim=1, unbiased=False), torch.ones(M), atol=1e-3)
+    # the f16 rounding of X is visible after normalisation: >= 4x the 2e-2 tolerance somewhere
+    x = O.gemm_bias_act_ref(d["A"], d["B"], d["bias"], "none")
+    x16 = x.half().float()
+    mean = x.mean(dim=1, keepdim=True)
+    rstd = torch.rsqrt(((x - mean) ** 2).mean(dim=1, keepdim=True) + 1e-5)
+    assert float(((x16 - x) * rstd).abs().max()) > 0.08
+    with pytest.raises(ValueError):
+        I.config3_offset(M, N, K, "nope")
