@@ -91,6 +91,13 @@ int plan_splits(int nkt, int block_k, int split_k, int* k_split) {
   return ceil_div(nkt, per);
 }
 
+FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint32_t p = 31 + l;
+  return FastDiv{(uint32_t)((1ull << p) / d + 1), p};
+}
+
 KArgs base_args() {
   KArgs a;
   memset(&a, 0, sizeof(a));
@@ -349,7 +356,8 @@ int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, con
   if (C % 8 || F % 8) return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: need C%%8==0 and F%%8==0 (C=%d F=%d)", C, F);
   const long long Mg = (long long)N * OH * OW;
   const long long Kg = (long long)KH * KW * C;
-  if (Mg > 0x7FFFFFFF || Kg % t.block_k || split_k > Kg / t.block_k)
+  // rows of the last M tile (up to tiles_m * block_m - 1) index the gather: they stay below 2^31
+  if (Mg > 0x7FFFFFFFll - t.block_m || Kg % t.block_k || split_k > Kg / t.block_k)
     return fail(ICPP_E_SHAPE, "icpp_conv2d_nhwc: K=%lld must be a multiple of block_k=%d with at least split_k=%d K tiles",
                 Kg, t.block_k, split_k);
   const unsigned long long xbytes = (unsigned long long)N * H * W * C * 2;
@@ -365,6 +373,13 @@ int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, con
   a.tiles_n = ceil_div(F, t.block_n);
   a.cH = H; a.cW = W; a.cC = C; a.cKH = KH; a.cKW = KW; a.cS = stride; a.cP = pad; a.cD = dilation; a.cOH = OH;
   a.cOW = OW;
+  a.dv_ohw = make_fastdiv((uint32_t)(OH * OW));
+  a.dv_ow = make_fastdiv((uint32_t)OW);
+  a.dv_w = make_fastdiv((uint32_t)W);
+  a.dv_wp = make_fastdiv((uint32_t)(W + 2));
+  a.dv_h = make_fastdiv((uint32_t)H);
+  a.tap_rows = 0;
+  for (int kh = 0; kh < KH && kh * KW < 32; ++kh) a.tap_rows |= 1u << (kh * KW);
   a.a_bytes_total = (uint32_t)xbytes;
   a.act = act;
   a.ce.flags = epi_flags;
@@ -380,7 +395,7 @@ int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, con
   const bool halo = in->launch_halo && KH == 3 && KW == 3 && stride == 1 && dilation == 1 && pad == 1 &&
                     C == t.block_k && a.splits == 1 && halo_rows * (W + 2) * 128 <= in->halo_bytes;
   const LaunchFn launch = halo ? in->launch_halo
-                               : (C % t.block_k == 0 && KH * KW <= 64) ? in->launch : in->launch_gather;
+                               : (C % t.block_k == 0 && KH * KW <= 32) ? in->launch : in->launch_gather;
   const dim3 grid(a.tiles_m * a.tiles_n * a.splits);  // one workgroup per (tile, K split) item
   if (a.splits > 1) {
     const size_t need = (size_t)split_k * a.M * F * sizeof(float);

@@ -40,9 +40,11 @@ enum DType { DT_F16 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_F32 = 3 };
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3, ACT_GELU_ERF = 4 };
 enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
 // A operand loaders: dense rows, the NHWC implicit-GEMM gather for any C
-// (per 16-byte chunk), and the gather for C % BK == 0, where every K tile is one
-// filter tap so the tap decomposition is per tile rather than per chunk.
-enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2, A_HALO = 3, A_DENSE_PP = 4 };
+// (per 16-byte chunk), the gather for C % BK == 0, where every K tile is one
+// filter tap so the tap decomposition is per tile rather than per chunk, and the
+// input halo of a 3x3 stride-1 conv tile.  A_PP, or-ed into a loader, selects the
+// ping-pong mainloop (8 waves in two groups of one wave per SIMD).
+enum ALoad { A_DENSE = 0, A_IM2COL = 1, A_IM2COL_TAP = 2, A_HALO = 3, A_PP = 8, A_DENSE_PP = A_DENSE | A_PP };
 // LDS bytes of the input halo of a BM-row A_HALO conv tile (see gemm_kernel): the rows
 // BM output pixels can span in an image of width <= 56, plus a one-row border on
 // each side, 58 columns, 128 B per pixel.  Launchers check the actual width fits.
@@ -76,6 +78,16 @@ struct ConvEpiArgs {
   const void* residual;  // [M, ldc] f16, the output's layout
 };
 
+// Division by a launch-constant divisor d >= 1 of 0 <= n < 2^31: floor(n * m / 2^p)
+// with p = 31 + ceil(log2 d) and m = floor(2^p / d) + 1 < 2^32 (Granlund and
+// Montgomery's round-up method: m * d - 2^p lies in [1, d] <= 2^(p - 31)).  The
+// launcher computes (m, p); a division is then one 64-bit multiply and a shift
+// instead of ~30 vector instructions.
+struct FastDiv { uint32_t m; uint32_t p; };
+__device__ __forceinline__ int fdiv(int n, FastDiv d) {
+  return (int)(((uint64_t)(uint32_t)n * d.m) >> d.p);
+}
+
 // Kernel arguments (passed by value; everything the launcher resolved on the host).
 struct KArgs {
   const void* A;
@@ -97,6 +109,8 @@ struct KArgs {
   int partial;        // 1: store fp32 partials to ws[split]
   // implicit-GEMM conv geometry (A_IM2COL*); GEMM M = Nb*OH*OW, K = KH*KW*C
   int cH, cW, cC, cKH, cKW, cS, cP, cD, cOH, cOW;
+  FastDiv dv_ohw, dv_ow, dv_w, dv_wp, dv_h;  // by OH*OW, OW, W, W+2, H
+  uint32_t tap_rows;       // bit kh*KW set for every filter row kh (KH*KW <= 32)
   uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
   ConvEpiArgs ce;          // fused conv epilogue (conv instances only)
   const void* residual;    // LayerNorm epilogues: [M, ldc] (output type) added before the statistics, or null
@@ -488,11 +502,12 @@ gemm_kernel(KArgs p) {
   // halo per tile -- the tile's output rows plus a one-pixel border, all C
   // channels -- loaded once before the mainloop; the K tiles are the 9 filter
   // taps, so the pipeline stages hold B only.
-  constexpr bool HALO = ALOAD == A_HALO;
-  // A_DENSE_PP: dense A with the ping-pong mainloop (two wave groups alternate
-  // between an MFMA phase and a memory phase)
-  constexpr bool DENSE = ALOAD == A_DENSE || ALOAD == A_DENSE_PP;
-  constexpr bool PP = ALOAD == A_DENSE_PP;
+  constexpr int LOADER = ALOAD & 7;
+  constexpr bool HALO = LOADER == A_HALO;
+  constexpr bool DENSE = LOADER == A_DENSE;
+  // A_PP: the ping-pong mainloop (two wave groups alternate between an MFMA phase
+  // and a memory phase)
+  constexpr bool PP = (ALOAD & A_PP) != 0;
   constexpr int HALO_CAP = halo_cap(BM);
   constexpr int SBYTES = HALO ? G::B_BYTES : G::STAGE_BYTES;  // bytes per stage array
   constexpr int A_OFF = HALO ? 0 : G::A_BYTES;                // B region offset in a stage
@@ -553,17 +568,19 @@ gemm_kernel(KArgs p) {
   __amdgpu_buffer_rsrc_t ra, rb;
   constexpr bool A_UNIFORM = DENSE && (G::THREADS % G::CPR_A == 0) &&
                              ((G::THREADS / G::CPR_A) % (G::RPB_A * G::SWZ_A) == 0);
-  constexpr bool B_UNIFORM = (G::THREADS % G::CPR_B == 0) && ((G::THREADS / G::CPR_B) % G::B_SWZ_PERIOD == 0);
+  // Conv tiles keep one VGPR offset per B load (B tiles are small there), so a tile's
+  // B loads share one scalar offset: no per-load scalar add in the issue-bound loop.
+  constexpr bool B_UNIFORM = DENSE && (G::THREADS % G::CPR_B == 0) && ((G::THREADS / G::CPR_B) % G::B_SWZ_PERIOD == 0);
   constexpr int NA = A_UNIFORM ? 1 : G::SA;
   constexpr int NB = B_UNIFORM ? 1 : G::SB;
-  constexpr bool GATHER = ALOAD == A_IM2COL, TAPS = ALOAD == A_IM2COL_TAP;
+  constexpr bool GATHER = LOADER == A_IM2COL, TAPS = LOADER == A_IM2COL_TAP;
   uint32_t a_goff[NA];  // per-lane A byte offset within the item's rows, K offset excluded
   // general gather: chunk column, image (-1 past M) and the (0, 0)-tap input coordinates
   int a_lc[GATHER ? G::SA : 1], a_img[GATHER ? G::SA : 1], a_ih0[GATHER ? G::SA : 1], a_iw0[GATHER ? G::SA : 1];
   // per-tile-tap gather: byte offset of the chunk at tap (0, 0) (may be negative
   // at the padding border) and the set of taps that land inside the image
   int a_tbase[TAPS ? G::SA : 1];
-  uint64_t a_tmask[TAPS ? G::SA : 1];
+  uint32_t a_tmask[TAPS ? G::SA : 1];  // bit t: tap t lands inside the image (KH * KW <= 32)
   // Point the loaders at item it: buffer descriptors at its rows / columns and,
   // for the conv gathers, each lane's input coordinates for its output row.
   auto setup_issue = [&](const Item& it) ICPP_INLINE {
@@ -587,10 +604,9 @@ gemm_kernel(KArgs p) {
       a_goff[i] = (uint32_t)(r * p.lda * ESZ + c * G::CH * ESZ);
     } else {
       const int m = row0 + r;
-      const int ohw = p.cOH * p.cOW;
-      const int img = m / ohw;
-      const int rem = m - img * ohw;
-      const int oh = rem / p.cOW, ow = rem - (rem / p.cOW) * p.cOW;
+      const int img = fdiv(m, p.dv_ohw);
+      const int rem = m - img * p.cOH * p.cOW;
+      const int oh = fdiv(rem, p.dv_ow), ow = rem - oh * p.cOW;
       const int ih0 = oh * p.cS - p.cP, iw0 = ow * p.cS - p.cP;
       if constexpr (GATHER) {
         a_lc[i] = c;
@@ -599,12 +615,24 @@ gemm_kernel(KArgs p) {
         a_iw0[i] = iw0;
       } else {
         a_tbase[i] = (((img * p.cH + ih0) * p.cW + iw0) * p.cC + c * G::CH) * ESZ;
-        uint64_t mk = 0;
+        uint32_t mk = 0;
         if (m < p.M) {
-          for (int tap = 0, kh = 0, kw = 0; tap < p.cKH * p.cKW; ++tap) {
-            const int ih = ih0 + kh * p.cD, iw = iw0 + kw * p.cD;
-            if ((unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW) mk |= 1ull << tap;
-            if (++kw == p.cKW) { kw = 0; ++kh; }
+          if (p.cD == 1) {
+            // the taps with 0 <= ih0 + kh < H and 0 <= iw0 + kw < W form a rectangle of the
+            // KH x KW grid: columns kw_lo..kw_hi replicated over rows kh_lo..kh_hi
+            const int kh_lo = max(0, -ih0), kh_hi = min(p.cKH - 1, p.cH - 1 - ih0);
+            const int kw_lo = max(0, -iw0), kw_hi = min(p.cKW - 1, p.cW - 1 - iw0);
+            if (kh_lo <= kh_hi && kw_lo <= kw_hi) {
+              const uint32_t cols = ((2u << kw_hi) - 1u) & ~((1u << kw_lo) - 1u);
+              const uint32_t rows = ((2u << ((kh_hi + 1) * p.cKW - 1)) - 1u) & ~((1u << (kh_lo * p.cKW)) - 1u);
+              mk = cols * (p.tap_rows & rows);
+            }
+          } else {
+            for (int tap = 0, kh = 0, kw = 0; tap < p.cKH * p.cKW; ++tap) {
+              const int ih = ih0 + kh * p.cD, iw = iw0 + kw * p.cD;
+              if ((unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW) mk |= 1u << tap;
+              if (++kw == p.cKW) { kw = 0; ++kh; }
+            }
           }
         }
         a_tmask[i] = mk;
@@ -645,9 +673,9 @@ gemm_kernel(KArgs p) {
       for (int tm = 0; tm < G::TM; ++tm) {
         int m = it.row0 + wm * G::WTM + tm * MF + (lane % MF);
         m = min(m, p.M - 1);  // rows past M compute on a valid pixel and are never stored
-        const int g = m / Wd;
+        const int g = fdiv(m, p.dv_w);
         const int ow = m - g * Wd;
-        const int oh = g % p.cH;
+        const int oh = g - fdiv(g, p.dv_h) * p.cH;
         h_q[tm] = (g - g0) * Wp + ow;
         h_vmask[tm] = (oh > 0 ? 1 : 0) | 2 | (oh < p.cH - 1 ? 4 : 0);
       }
@@ -665,7 +693,7 @@ gemm_kernel(KArgs p) {
         const int s = i * G::THREADS + tid;
         if (s < nslots) {
           const int q = s >> 3;
-          const int hr = q / Wp;
+          const int hr = fdiv(q, p.dv_wp);
           const int hc = q - hr * Wp;
           const int grow = g0 - 1 + hr;
           const int iw = hc - 1;
@@ -680,29 +708,71 @@ gemm_kernel(KArgs p) {
   const uint32_t a_row_step = (uint32_t)((G::THREADS / G::CPR_A) * p.lda * ESZ);  // bytes per load (A_UNIFORM)
   const uint32_t b_row_step = (uint32_t)((G::THREADS / G::CPR_B) * p.ldb * ESZ);  // bytes per load (B_UNIFORM)
 
-  // Per-tile part of the A address shared by all loads of the tile starting at
-  // K element kk.  For the per-tile-tap gather (C % BK == 0) that tile is filter
-  // tap `tap` and channels c0 .. c0+BK-1 of it: scalar work once per tile, after
-  // which a lane's offset is its tap-(0,0) base plus a tile constant, or past
-  // the buffer (zeros) when the tap falls in the padding.
+  // Per-tile part of the A address shared by all loads of a K tile.  For the
+  // per-tile-tap gather (C % BK == 0) that tile is filter tap `tap` and channels
+  // c0 .. c0+BK-1 of it, and a lane's offset is its tap-(0,0) base plus the tile
+  // constant toff, or past the buffer (zeros) when the tap falls in the padding.
+  // The issue cursor carries (tap, filter column, c0, tap byte offset) from tile to
+  // tile with adds and selects: one wave issues one instruction per 4 cycles, so
+  // the two runtime divisions a K index -> (tap, c0) decomposition costs (~60
+  // scalar instructions) would outlast the tile's MFMAs.
   struct TileCtx { int tap; int toff; };
-  auto tile_ctx = [&](int kk) ICPP_INLINE {
-    TileCtx t{0, 0};
+  int t_tap = 0, t_kw = 0, t_c0 = 0, t_off = 0, t_col_step = 0, t_row_step = 0;
+  if constexpr (TAPS) {
+    const int kg = (first.kz * p.k_split) / BK;  // the item's first K tile
+    const int tiles_per_tap = p.cC / BK;
+    t_tap = kg / tiles_per_tap;
+    t_c0 = (kg - t_tap * tiles_per_tap) * BK;
+    const int kh = t_tap / p.cKW;
+    t_kw = t_tap - kh * p.cKW;
+    t_off = (kh * p.cD * p.cW + t_kw * p.cD) * p.cC * ESZ;
+    t_col_step = p.cD * p.cC * ESZ;                              // (kh, kw) -> (kh, kw + 1)
+    t_row_step = (p.cD * p.cW - (p.cKW - 1) * p.cD) * p.cC * ESZ;  // (kh, KW - 1) -> (kh + 1, 0)
+    // wave-uniform by construction; said so, the scalar cursor below may hold them in SGPRs
+    t_tap = __builtin_amdgcn_readfirstlane(t_tap);
+    t_c0 = __builtin_amdgcn_readfirstlane(t_c0);
+    t_kw = __builtin_amdgcn_readfirstlane(t_kw);
+    t_off = __builtin_amdgcn_readfirstlane(t_off);
+    t_col_step = __builtin_amdgcn_readfirstlane(t_col_step);
+    t_row_step = __builtin_amdgcn_readfirstlane(t_row_step);
+  }
+  auto cursor_ctx = [&]() ICPP_INLINE { return TileCtx{t_tap, t_off + t_c0 * ESZ}; };
+  // The tap cursor one K tile on.  Past the item's last tile it keeps going: the
+  // issue index of B is clamped (a cached re-read), and A's tap runs past KH * KW
+  // (at most STAGES - 1 taps, so below 32), whose mask bits are 0 -- those loads
+  // take the out-of-range offset and return zeros, into stages nobody reads.
+  // Written as scalar instructions: the state is wave-uniform, but compiled from C++
+  // the compare-and-increment becomes a vector add-with-carry and the cursor moves
+  // into VGPRs (~17 vector instructions per tile).  12 scalar ones here:
+  //   c0 += BK; w = (c0 == C); c0 = w ? 0 : c0; tap += w; kw += w; off += w ? col : 0;
+  //   r = (kw == KW); kw = r ? 0 : kw; off += r ? row - col : 0.
+  const int t_rmc = t_row_step - t_col_step;
+  auto cursor_step = [&]() ICPP_INLINE {
     if constexpr (TAPS) {
-      const int kg = kk / BK;  // global K-tile index
-      const int tiles_per_tap = p.cC / BK;
-      const int tap = kg / tiles_per_tap;
-      const int c0 = (kg - tap * tiles_per_tap) * BK;
-      const int kh = tap / p.cKW, kw = tap - (tap / p.cKW) * p.cKW;
-      t.tap = tap;
-      t.toff = ((kh * p.cD * p.cW + kw * p.cD) * p.cC + c0) * ESZ;
+      int t1, w;
+      asm volatile(
+          "s_add_i32 %0, %0, %6\n\t"
+          "s_cmp_eq_u32 %0, %7\n\t"
+          "s_cselect_b32 %0, 0, %0\n\t"
+          "s_cselect_b32 %4, %8, 0\n\t"
+          "s_cselect_b32 %5, 1, 0\n\t"
+          "s_add_i32 %1, %1, %5\n\t"
+          "s_add_i32 %2, %2, %5\n\t"
+          "s_add_i32 %3, %3, %4\n\t"
+          "s_cmp_eq_u32 %2, %9\n\t"
+          "s_cselect_b32 %2, 0, %2\n\t"
+          "s_cselect_b32 %4, %10, 0\n\t"
+          "s_add_i32 %3, %3, %4"
+          : "+s"(t_c0), "+s"(t_tap), "+s"(t_kw), "+s"(t_off), "=&s"(t1), "=&s"(w)
+          : "s"(BK), "s"(__builtin_amdgcn_readfirstlane(p.cC)), "s"(t_col_step),
+            "s"(__builtin_amdgcn_readfirstlane(p.cKW)), "s"(__builtin_amdgcn_readfirstlane(t_rmc))
+          : "scc");
     }
-    return t;
   };
   // One 16-byte-per-lane load of the tile at K element kk into stage S: loads
   // 0 .. SA-1 move A chunks, SA .. SA+SB-1 move B chunks.  Issued one at a time
   // so the mainloop can spread them between the MFMAs of the tile being multiplied.
-  auto issue_load = [&](int kk, auto S, auto L, const TileCtx& tc) ICPP_INLINE {
+  auto issue_load = [&](int kk, auto S, auto L, const TileCtx& tc, uint32_t boff) ICPP_INLINE {
     constexpr int l = decltype(L)::value;
     char ICPP_LDS* as = stage_base(S);
     char ICPP_LDS* bs = as + A_OFF;
@@ -715,7 +785,7 @@ gemm_kernel(KArgs p) {
         else
           dma16(ra, a_goff[i], (uint32_t)(kk * ESZ), as + i * G::THREADS * 16 + wave_slot);
       } else if constexpr (TAPS) {
-        const bool ok = (a_tmask[i] >> tc.tap) & 1u;
+        const bool ok = (a_tmask[i] >> tc.tap) & 1u;  // tc.tap < 32
         const uint32_t off = ok ? (uint32_t)(a_tbase[i] + tc.toff) : p.a_bytes_total;
         dma16(ra, off, 0u, as + i * G::THREADS * 16 + wave_slot);
       } else {
@@ -734,15 +804,15 @@ gemm_kernel(KArgs p) {
       constexpr int i = l - LA;
       if (!(G::B_EVEN || tid + i * G::THREADS < G::B_CHUNKS)) return;
       if constexpr (B_UNIFORM)
-        dma16(rb, b_goff[0], (uint32_t)(kk * p.ldb * ESZ) + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
+        dma16(rb, b_goff[0], boff + i * b_row_step, bs + i * G::THREADS * 16 + wave_slot);
       else
-        dma16(rb, b_goff[i], (uint32_t)(kk * p.ldb * ESZ), bs + i * G::THREADS * 16 + wave_slot);
+        dma16(rb, b_goff[i], boff, bs + i * G::THREADS * 16 + wave_slot);
     }
   };
   constexpr int LOADS = LA + G::SB;  // loads per thread per tile
-  auto issue_tile = [&](int kk, auto S) ICPP_INLINE {
-    const TileCtx tc = tile_ctx(kk);
-    static_for<LOADS>([&](auto L) ICPP_INLINE { issue_load(kk, S, L, tc); });
+  // boff: byte offset of the tile's first B row (kk * ldb * ESZ)
+  auto issue_tile = [&](int kk, auto S, const TileCtx& tc, uint32_t boff) ICPP_INLINE {
+    static_for<LOADS>([&](auto L) ICPP_INLINE { issue_load(kk, S, L, tc, boff); });
   };
 
   Acc acc[G::TM][G::TN];
@@ -1276,13 +1346,29 @@ gemm_kernel(KArgs p) {
   // cached re-read into a stage nobody reads again), so every step issues
   // exactly LOADS loads.
   int cur_kt = 0;
-  auto advance_issue = [&]() ICPP_INLINE { cur_kt = min(cur_kt + 1, nk - 1); };
+  // Conv tiles: the B byte offset of the issue cursor, advanced by one tile of rows
+  // without the clamp (past K the loads fall outside B's range and return zeros;
+  // past a split-K slice they read the next slice's rows; either lands in a stage
+  // nobody reads).  Dense tiles compute it from the clamped cursor.
+  uint32_t t_boff = (uint32_t)(first.kz * p.k_split * p.ldb * ESZ);
+  const uint32_t t_bstep = (uint32_t)(BK * p.ldb * ESZ);
+  auto advance_issue = [&]() ICPP_INLINE {
+    cur_kt = min(cur_kt + 1, nk - 1);
+    cursor_step();
+    if constexpr (!DENSE) t_boff += t_bstep;
+  };
   auto cur_kk = [&]() ICPP_INLINE { return first.kz * p.k_split + cur_kt * BK; };
+  auto cur_boff = [&]() ICPP_INLINE {
+    if constexpr (DENSE) return (uint32_t)(cur_kk() * p.ldb * ESZ);
+    else return t_boff;
+  };
 
   // K tile -> filter tap for A_HALO (C == BK: the K tiles are the taps; clamped for the
   // prefetch past the last tile, whose fragments are never used)
   const int kt_base = (first.kz * p.k_split) / BK;
   auto tap_of = [&](int kt) ICPP_INLINE { return HALO ? min(kt_base + kt, 8) : 0; };
+  setup_halo(first);
+  issue_halo(first);  // older than every B load: landed once tile 0 has
   if constexpr (PP) {
     // ---- ping-pong mainloop ----------------------------------------------------
     // Waves w and w + 4 share a SIMD, and group g = wm holds one wave per SIMD.
@@ -1298,15 +1384,19 @@ gemm_kernel(KArgs p) {
     // tiles are in flight -- tile j+1 has landed -- so the barrier ending phase
     // 2j+1 publishes it.  Barriers per wave: 2 nk (phases 0 .. 2nk-1); group 1's
     // last MFMA phase (2nk) has none and runs while group 0 reaches the epilogue.
-    static_assert(WM == 2 && WN == 4 && STAGES >= 2 && EPI == EPI_STORE,
-                  "ping-pong: 2 x 4 waves (one wave of each group per SIMD), store epilogue");
+    // Group g = wave / 4: waves w and w + 4 share a SIMD whatever the 8-wave grid.
+    // Each wave issues the tiles in order (group 1 one tile ahead of group 0), so
+    // the conv loaders take the next tile from the issue cursor.
+    static_assert(WM * WN == 8 && STAGES >= 2 && EPI == EPI_STORE,
+                  "ping-pong: 8 waves (one wave of each group per SIMD), store epilogue");
     // The fragments of one tile live from its memory phase to its MFMA phase of
     // the same iteration only; the accumulators are the only loop-carried state.
-    auto read_tile = [&](auto J, Frag (&fa_)[NKS][G::TM], Frag (&fb_)[NKS][G::TN]) ICPP_INLINE {
+    auto read_tile = [&](auto J, int kt, Frag (&fa_)[NKS][G::TM], Frag (&fb_)[NKS][G::TN]) ICPP_INLINE {
       const char ICPP_LDS* as = stage_base(J);
+      const int tap = tap_of(kt);
       static_for<NKS>([&](auto KS) ICPP_INLINE {
         constexpr int ks = decltype(KS)::value;
-        load_frags(as, as + A_OFF, KS, fa_[ks], fb_[ks], 0);
+        load_frags(as, as + A_OFF, KS, fa_[ks], fb_[ks], tap);
       });
     };
     auto mfma_tile = [&](Frag (&fa_)[NKS][G::TM], Frag (&fb_)[NKS][G::TN]) ICPP_INLINE {
@@ -1345,11 +1435,21 @@ gemm_kernel(KArgs p) {
     // re-read into a stage nobody reads again), so every even phase issues LOADS loads
     const int kbase = first.kz * p.k_split;
     auto tile_k = [&](int t) ICPP_INLINE { return kbase + min(t, nk - 1) * BK; };
+    auto tile_boff = [&](int t) ICPP_INLINE { return (uint32_t)(tile_k(t) * p.ldb * ESZ); };
+    // issue tile t (this wave's next) into stage ST
+    auto issue_seq = [&](auto ST, int t) ICPP_INLINE {
+      if constexpr (DENSE) {
+        issue_tile(tile_k(t), ST, TileCtx{0, 0}, tile_boff(t));
+      } else {
+        issue_tile(cur_kk(), ST, cursor_ctx(), cur_boff());
+        advance_issue();
+      }
+    };
     constexpr int S = STAGES;
-    static_for<S - 1>([&](auto I) ICPP_INLINE { issue_tile(tile_k(decltype(I)::value), I); });
+    static_for<S - 1>([&](auto I) ICPP_INLINE { issue_seq(I, decltype(I)::value); });
     wait_tiles(std::integral_constant<int, S - 2>{});  // this wave's loads of tile 0 landed
     lds_barrier();                                     // tile 0 published
-    if (__builtin_amdgcn_readfirstlane(wm) == 0) {
+    if (__builtin_amdgcn_readfirstlane(wave) < 4) {
       for (int kt0 = 0; kt0 < nk; kt0 += S) {
         static_for<S>([&](auto J) ICPP_INLINE {
           constexpr int j = decltype(J)::value;
@@ -1357,8 +1457,8 @@ gemm_kernel(KArgs p) {
           if (kt < nk) {
             Frag fa_[NKS][G::TM], fb_[NKS][G::TN];
             // phase 2kt: issue tile kt+S-1, read tile kt
-            issue_tile(tile_k(kt + S - 1), std::integral_constant<int, (j + S - 1) % S>{});
-            read_tile(J, fa_, fb_);
+            issue_seq(std::integral_constant<int, (j + S - 1) % S>{}, kt + S - 1);
+            read_tile(J, kt, fa_, fb_);
             sched_mem();
             phase_end();
             // phase 2kt+1: multiply tile kt; then this wave's loads of tile kt+1 have landed
@@ -1374,7 +1474,7 @@ gemm_kernel(KArgs p) {
         });
       }
     } else {
-      issue_tile(tile_k(S - 1), std::integral_constant<int, S - 1>{});
+      issue_seq(std::integral_constant<int, S - 1>{}, S - 1);
       phase_end();  // phase 0: group 1 has nothing to multiply yet
       for (int kt0 = 0; kt0 < nk; kt0 += S) {
         static_for<S>([&](auto J) ICPP_INLINE {
@@ -1383,12 +1483,12 @@ gemm_kernel(KArgs p) {
           if (kt < nk) {
             Frag fa_[NKS][G::TM], fb_[NKS][G::TN];
             // phase 2kt+1: read tile kt; this wave's loads of tile kt+1 have landed
-            read_tile(J, fa_, fb_);
+            read_tile(J, kt, fa_, fb_);
             __builtin_amdgcn_sched_barrier(0);
             wait_tiles(std::integral_constant<int, S - 2>{});
             phase_end();
             // phase 2kt+2: multiply tile kt; issue tile kt+S into the stage tile kt leaves
-            issue_tile(tile_k(kt + S), J);
+            issue_seq(J, kt + S);
             mfma_tile(fa_, fb_);
             sched_mfma(std::integral_constant<int, LOADS>{});
             if (kt + 1 < nk) phase_end();
@@ -1397,11 +1497,9 @@ gemm_kernel(KArgs p) {
       }
     }
   } else {
-  setup_halo(first);
-  issue_halo(first);  // older than every B load: landed once tile 0 has
   static_for<STAGES>([&](auto S) ICPP_INLINE {
     if constexpr (decltype(S)::value > 0) advance_issue();
-    issue_tile(cur_kk(), S);
+    issue_tile(cur_kk(), S, cursor_ctx(), cur_boff());
   });
   wait_tiles(std::integral_constant<int, STAGES - 1>{});  // this wave's loads of tile 0 landed
   lds_barrier();  // tile 0 published
@@ -1423,7 +1521,7 @@ gemm_kernel(KArgs p) {
         advance_issue();                      // cursor -> step kt+STAGES (clamped)
         wait_tiles(std::integral_constant<int, STAGES - 2>{});  // this wave's loads of tile kt+1 landed
         lds_barrier();                        // B(kt): tile kt+1 published, stage j retired
-        issue_tile(cur_kk(), J);
+        issue_tile(cur_kk(), J, cursor_ctx(), cur_boff());
         constexpr int jn = (j + 1) % STAGES;
         const char ICPP_LDS* an = stage_base(std::integral_constant<int, jn>{});
         load_frags(an, an + A_OFF, std::integral_constant<int, 0>{}, fa[(s + 1) & 1], fb[(s + 1) & 1],

@@ -51,11 +51,12 @@ Instance make_instance(int family, const char* name) {
   in.epi = EPI;
   in.aload = AL;
   in.wave_tile_n = G::WTN;
-  if constexpr (AL == A_IM2COL) {
-    in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL_TAP>;
-    in.launch_gather = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL>;
+  if constexpr ((AL & 7) == A_IM2COL) {
+    constexpr int PPB = AL & A_PP;  // the schedule bit carries over to every conv loader
+    in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL_TAP | PPB>;
+    in.launch_gather = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_IM2COL | PPB>;
     constexpr bool halo_fits = G::ESZ == 2 && BK == 64 && G::B_BYTES * ST + halo_cap(BM) <= 160 * 1024;
-    if constexpr (halo_fits) in.launch_halo = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_HALO>;
+    if constexpr (halo_fits) in.launch_halo = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, A_HALO | PPB>;
     else in.launch_halo = nullptr;
     in.halo_bytes = halo_cap(BM);
   } else {

@@ -17,10 +17,11 @@ Families
 Mainloop schedules (``sched``)
   ""            every wave streams MFMAs and its fragment reads together; one
                 workgroup barrier per K tile
-  "pp"          ping-pong (2 x 4 waves, gemm family): the wave group of each row
-                half alternates between an MFMA-only phase and a memory phase
-                (fragment reads + tile loads), offset by one phase from the other
-                group, so the two waves of a SIMD never split its matrix core
+  "pp"          ping-pong (8 waves, gemm and conv2d families): each group of four
+                waves (one per SIMD) alternates between an MFMA-only phase and a
+                memory phase (fragment reads + tile loads), offset by one phase from
+                the other group, so the two waves of a SIMD never split its matrix
+                core and one issues memory instructions while the other's MFMAs run
 """
 
 from __future__ import annotations
@@ -104,8 +105,8 @@ class Inst:
             problems.append("too many loads in flight for vmcnt")
         if self.sched not in ("", "pp"):
             problems.append("unknown mainloop schedule")
-        if self.sched == "pp" and (self.family != "gemm" or (self.wm, self.wn) != (2, 4)):
-            problems.append("ping-pong needs the gemm family and a 2 x 4 wave grid")
+        if self.sched == "pp" and (self.family not in ("gemm", "conv2d") or self.wm * self.wn != 8):
+            problems.append("ping-pong needs the gemm or conv2d family and 8 waves")
         if problems:
             raise ValueError(f"{self.name}: " + "; ".join(problems))
 
@@ -227,11 +228,33 @@ def _conv_tiles() -> List[Inst]:
         _g("f16", 128, 128, 32, 2, 2, 16, st=4, fam=c),
         _g("f16", 64, 128, 64, 1, 4, 16, st=4, fam=c),
         _g("f16", 256, 128, 64, 2, 4, 16, fam=c),
+        # ping-pong conv tiles: with one wave per SIMD a K tile costs about three times
+        # its MFMA time in issue slots and exposed waits; two waves per SIMD in
+        # alternating MFMA / memory phases overlap them
+        Inst(c, "f16", 64, 128, 64, 2, 4, 16, 4, "pp"),
+        Inst(c, "f16", 64, 128, 64, 2, 4, 16, 3, "pp"),
+        Inst(c, "f16", 128, 64, 64, 2, 4, 16, 4, "pp"),
+        Inst(c, "f16", 128, 64, 64, 4, 2, 16, 4, "pp"),
+        Inst(c, "f16", 64, 64, 64, 2, 4, 16, 4, "pp"),
+        Inst(c, "f16", 128, 128, 64, 2, 4, 16, 3, "pp"),
+        Inst(c, "f16", 256, 64, 64, 4, 2, 16, 2, "pp"),
+        Inst(c, "f16", 256, 64, 64, 8, 1, 32, 2, "pp"),
+        Inst(c, "f16", 224, 64, 64, 2, 4, 16, 2, "pp"),
         # row-aligned / deeper tiles for wide images under the input-halo loader
         # (224 = 4 rows of 56; 8 waves on 256 rows)
         _g("f16", 256, 64, 64, 4, 2, 16, fam=c),
         _g("f16", 224, 64, 64, 2, 2, 16, fam=c),
         _g("f16", 224, 64, 64, 7, 1, 32, fam=c),
+        # small conv grids (98-196 tiles for 256 CUs) run one wave per SIMD, which issues
+        # one instruction per 4 cycles: 32x32x16 MFMAs (32 cycles each) and 128-deep K
+        # tiles leave more issue slots per MFMA for the fragment reads and tile loads
+        _g("f16", 64, 128, 64, 1, 4, 32, st=4, fam=c),
+        _g("f16", 64, 128, 64, 2, 2, 32, st=4, fam=c),
+        _g("f16", 128, 64, 64, 2, 2, 32, st=4, fam=c),
+        _g("f16", 128, 64, 64, 4, 1, 32, st=4, fam=c),
+        _g("f16", 64, 128, 128, 1, 4, 32, st=3, fam=c),
+        _g("f16", 128, 64, 128, 2, 2, 32, st=3, fam=c),
+        _g("f16", 64, 64, 128, 2, 2, 16, st=4, fam=c),
     ]
 
 
