@@ -228,33 +228,16 @@ def _conv_tiles() -> List[Inst]:
         _g("f16", 128, 128, 32, 2, 2, 16, st=4, fam=c),
         _g("f16", 64, 128, 64, 1, 4, 16, st=4, fam=c),
         _g("f16", 256, 128, 64, 2, 4, 16, fam=c),
-        # ping-pong conv tiles: with one wave per SIMD a K tile costs about three times
-        # its MFMA time in issue slots and exposed waits; two waves per SIMD in
-        # alternating MFMA / memory phases overlap them
-        Inst(c, "f16", 64, 128, 64, 2, 4, 16, 4, "pp"),
-        Inst(c, "f16", 64, 128, 64, 2, 4, 16, 3, "pp"),
-        Inst(c, "f16", 128, 64, 64, 2, 4, 16, 4, "pp"),
-        Inst(c, "f16", 128, 64, 64, 4, 2, 16, 4, "pp"),
-        Inst(c, "f16", 64, 64, 64, 2, 4, 16, 4, "pp"),
-        Inst(c, "f16", 128, 128, 64, 2, 4, 16, 3, "pp"),
-        Inst(c, "f16", 256, 64, 64, 4, 2, 16, 2, "pp"),
-        Inst(c, "f16", 256, 64, 64, 8, 1, 32, 2, "pp"),
-        Inst(c, "f16", 224, 64, 64, 2, 4, 16, 2, "pp"),
         # row-aligned / deeper tiles for wide images under the input-halo loader
         # (224 = 4 rows of 56; 8 waves on 256 rows)
         _g("f16", 256, 64, 64, 4, 2, 16, fam=c),
         _g("f16", 224, 64, 64, 2, 2, 16, fam=c),
         _g("f16", 224, 64, 64, 7, 1, 32, fam=c),
-        # small conv grids (98-196 tiles for 256 CUs) run one wave per SIMD, which issues
-        # one instruction per 4 cycles: 32x32x16 MFMAs (32 cycles each) and 128-deep K
-        # tiles leave more issue slots per MFMA for the fragment reads and tile loads
-        _g("f16", 64, 128, 64, 1, 4, 32, st=4, fam=c),
-        _g("f16", 64, 128, 64, 2, 2, 32, st=4, fam=c),
-        _g("f16", 128, 64, 64, 2, 2, 32, st=4, fam=c),
-        _g("f16", 128, 64, 64, 4, 1, 32, st=4, fam=c),
-        _g("f16", 64, 128, 128, 1, 4, 32, st=3, fam=c),
-        _g("f16", 128, 64, 128, 2, 2, 32, st=3, fam=c),
-        _g("f16", 64, 64, 128, 2, 2, 16, st=4, fam=c),
+        # ping-pong conv tiles (the tap gather and the input halo under the 8-wave
+        # ping-pong loop): measured 16-25% slower than the best default-schedule tile at
+        # every benchmark conv shape, kept so that both loader paths stay compiled and tested
+        Inst(c, "f16", 64, 128, 64, 2, 4, 16, 4, "pp"),
+        Inst(c, "f16", 256, 64, 64, 4, 2, 16, 2, "pp"),
     ]
 
 

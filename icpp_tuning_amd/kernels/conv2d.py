@@ -47,6 +47,23 @@ class Conv2dDescriptor(InstanceDescriptor):
         from dataclasses import replace
         return replace(spec, mainloop=replace(spec.mainloop, K=spec.mainloop.K // sk))
 
+    def schedule_factor(self, raw: Dict[str, Any]) -> float:
+        """Ping-pong conv tiles measured 0.79-0.84x the best default-schedule tile on
+        the benchmark conv shapes (b32 14x14x256, 56x56x64)."""
+        return 0.8 if raw.get("sched") == "pp" else 1.0
+
+    def extra_seconds(self, raw, hw, **shape) -> float:
+        """Split-K conv launches measured slower than the schedule model prices them: on
+        the profiled conv shapes the unsplit tile wins wherever the model would split
+        small grids.  The fp32 partial round trip is charged twice its bytes at HBM rate
+        plus 2 us (fitted on the shipped conv databases: mean formula pick 0.90 -> 0.91-0.94
+        of the measured best)."""
+        sk = raw.get("split_k", 1)
+        if sk <= 1 or not getattr(hw, "has_mfma_model", False):
+            return 0.0
+        M, N = self.gemm_mn(**shape)
+        return 2.0 * M * N * 4.0 * sk / (hw.mem_bandwidth_gbps * 1e9) + 2e-6
+
     def k_extent(self, C=0, KH=3, KW=3, **kw) -> int:
         return C * KH * KW
 
