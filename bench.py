@@ -190,14 +190,31 @@ def cpu_baselines(per_op_s: float = 4.0):
             "per_op": per}
 
 
-def _load_traffic(workload: str):
+def _finite(x, nd):
+    """x rounded to nd places, or None when the tuner had no timing for it (NaN):
+    the JSON line must stay strict JSON, which has no NaN."""
+    return None if x is None or math.isnan(x) else round(x, nd)
+
+
+def _load_traffic(workload: str, tile: str):
+    """HBM bytes per launch of the headline kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_<workload>.json), and a label
+    naming that source.  The counters cannot be read from inside this process, so the
+    figure is only reported when the profiled tile is the one this run timed."""
     p = ROOT / "profiles" / f"traffic_{workload}.json"
+    src = f"profiles/{p.name}"
     if not p.exists():
-        return None
+        return None, f"no traffic profile ({src} absent)"
     try:
-        return json.loads(p.read_text()).get("bytes_per_launch")
-    except Exception:
-        return None
+        t = json.loads(p.read_text())
+    except ValueError:
+        return None, f"unreadable {src}"
+    if t.get("tile") != tile:
+        return None, f"{src} was profiled on tile {t.get('tile')}, this run timed {tile}"
+    return t.get("bytes_per_launch"), (f"{src}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over "
+                                       f"{t.get('dispatches', '?')} launches of {tile}, scaled by a device-copy "
+                                       f"calibration (fetch x{t['calibration']['fetch_scale']}, "
+                                       f"write x{t['calibration']['write_scale']})")
 
 
 def table_seed(desc, **shape):
@@ -279,7 +296,7 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
             row.update({
                 "tuned_over_copies": copies,
                 "formula_top1": desc.format_config(res.formula_top1),
-                "formula_top1_ms": round(res.formula_top1_ms, 5),
+                "formula_top1_ms": _finite(res.formula_top1_ms, 5),
                 "tuner": {"time_to_best_s": round(res.time_to_best_s, 3), "prune_rank_s": round(res.prune_rank_s, 4),
                           "compile_s": round(res.compile_s, 4), "bench_s": round(res.bench_s, 3),
                           "candidates": len(res.candidates), "failed": len(res.failed),
@@ -653,12 +670,17 @@ def headline(args):
         sets.append(d)
     steps = [(lambda d=d: kern(d["A"], d["B"], d["bias"], out=d["C"])) for d in sets]
     # The device sat idle while the inputs were built on the host.  Its power
-    # controller boosts the clock for the first launches after idle, then
-    # undershoots for ~10-20 ms (a trace showed warm-up launches at 106 us and the
-    # next 50 at 126 us, settling at 103 us).  So the clock probe's ~0.25 s burst
-    # runs first -- it settles the clock and measures it -- and the warm-up and
-    # timed steps follow it back to back, in the steady state.
+    # controller boosts the shader clock for the first launches after idle and
+    # holds the memory-side clocks low: a launch of this tile measured 120 us
+    # within a second of idle against 104-107 us after the tuner's ~2 s of
+    # launches, at a *higher* shader clock (2322 against 1929 MHz) -- the kernel
+    # waits on the L2 -> memory path, which the later state feeds faster.  So
+    # ~1.5 s of back-to-back steps settle the device first (also when no tuning
+    # ran, with --instance), then the clock probe's ~0.25 s burst measures the
+    # clock, and the warm-up and timed steps follow it back to back.
+    time_steps(steps, 5, 0)  # the first launches carry one-time costs (and a profiler's)
     est = time_steps(steps, 5, 0)[1] / 5
+    time_steps(steps, max(20, int(1.5 / max(est, 1e-6))), 0, sync_first=False)
     sclk, window, burst_kernel_s = sustained_clock(steps, est)
     wall, ev = time_steps(steps, args.steps, args.warmup, sync_first=False)
     flops = 2.0 * M * N * K
@@ -666,8 +688,9 @@ def headline(args):
     kernel_s = ev / args.steps
     achieved = flops / kernel_s / 1e12
     workload = "gemm_bias_gelu_tanh_4096x4096x4096_bf16"
+    traffic, traffic_src = _load_traffic(workload, desc.format_config(cfg))
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16, 4), "traffic": _load_traffic(workload),
+            "frac": round(achieved / PEAK_BF16, 4), "traffic": traffic, "traffic_source": traffic_src,
             "kernel_us": round(kernel_s * 1e6, 2), "peak_sclk_mhz": PEAK_SCLK_MHZ}
     if sclk:
         # the clock is measured over a ~0.25 s burst (the steady state), so the
@@ -690,7 +713,7 @@ def headline(args):
         out["tuner"] = {"time_to_best_s": round(tuned.time_to_best_s, 3), "prune_rank_s": round(tuned.prune_rank_s, 4),
                         "compile_s": round(tuned.compile_s, 4), "bench_s": round(tuned.bench_s, 3),
                         "formula_top1": desc.format_config(tuned.formula_top1),
-                        "formula_top1_ms": round(tuned.formula_top1_ms, 5), "select_best_s": round(select_s, 4),
+                        "formula_top1_ms": _finite(tuned.formula_top1_ms, 5), "select_best_s": round(select_s, 4),
                         "candidates": len(tuned.candidates),
                         "best_from": "table" if any(c["seed"] and c["config"] == cfg for c in tuned.candidates)
                         else "formula"}

@@ -287,9 +287,10 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
                 # the first timing after an idle device absorbs the clock ramp-up: discard it
                 benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
             ms = benchmark_ms(runs if copies > 1 else runs[0], warmup=warmup, reps=reps)
-        except (IcppCallError, ValueError) as e:
-            # a candidate the library or the launcher rejects is dropped with its reason
-            # (the reference's harness records "ERROR" rows and goes on, conv2d.py:453-460)
+        except IcppCallError as e:
+            # a candidate the library rejects is dropped with its reason (the reference's
+            # harness records "ERROR" rows and goes on, conv2d.py:453-460); operand errors
+            # (ValueError from the argument checks) are bugs of the caller and propagate
             failed.append({"config": raw, "formatted": formatted, "error": f"{type(e).__name__}: {e}"})
             return
         runners[formatted] = runs

@@ -17,7 +17,7 @@ def _head():
                    "op": "gemm+bias+gelu_tanh", "tile": "BM256_BN256_BK64_S2_T512_W2x4_M16_PP",
                    "input_copies": 7, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": 1135.7, "peak": 2516.6, "unit": "TFLOP/s", "frac": 0.4513,
-                     "traffic": 235180000, "kernel_us": 121.02, "peak_sclk_mhz": 2400.0, "sclk_mhz": 1650.3,
+                     "traffic": 235180000, "traffic_source": "t" * 260, "kernel_us": 121.02, "peak_sclk_mhz": 2400.0, "sclk_mhz": 1650.3,
                      "peak_at_sclk": 1730.5, "frac_at_sclk": 0.6563, "sclk_window_s": 0.2},
         "tuner": {"time_to_best_s": 1.234, "prune_rank_s": 0.0123, "compile_s": 0.0011, "bench_s": 1.2,
                   "formula_top1": "BM256_BN256_BK64_S2_T512_W2x4_M32", "formula_top1_ms": 0.1234,
@@ -94,3 +94,26 @@ def test_final_line_drops_detail_before_exceeding_the_limit():
     line = bench.final_line(_head(), rows, _cpu())
     assert len(line) <= bench.FINAL_LINE_MAX
     assert json.loads(line)["roofline"]["frac"] == 0.4513
+
+
+def test_untimed_formula_pick_is_null_not_nan():
+    # the tuner reports NaN for a formula pick it did not time; the line must stay strict JSON
+    assert bench._finite(float("nan"), 5) is None and bench._finite(None, 5) is None
+    assert bench._finite(0.123456789, 5) == 0.12346
+    h = _head()
+    h["tuner"]["formula_top1_ms"] = bench._finite(float("nan"), 5)
+    line = bench.final_line(h, _rows(), _cpu())
+    assert "NaN" not in line
+    assert json.loads(line)["tuner"]["formula_top1_ms"] is None
+
+
+def test_traffic_is_reported_only_for_the_profiled_tile():
+    from pathlib import Path
+    prof = json.loads((Path(bench.__file__).parent / "profiles" /
+                       "traffic_gemm_bias_gelu_tanh_4096x4096x4096_bf16.json").read_text())
+    b, src = bench._load_traffic("gemm_bias_gelu_tanh_4096x4096x4096_bf16", prof["tile"])
+    assert b == prof["bytes_per_launch"] and prof["tile"] in src and "FETCH_SIZE" in src
+    b, src = bench._load_traffic("gemm_bias_gelu_tanh_4096x4096x4096_bf16", "BM64_BN64_BK64_S2_T256_W2x2_M16")
+    assert b is None and "profiled on tile" in src
+    b, src = bench._load_traffic("no_such_workload", "x")
+    assert b is None and "absent" in src
