@@ -102,9 +102,27 @@ def test_failing_candidate_is_dropped_with_its_reason(monkeypatch, fake_device):
     assert "injected" in r.failed[0]["error"]
     assert bad not in [c["config"] for c in r.candidates] and len(r.candidates) == 3
 
-    monkeypatch.setattr(d, "make_runner", lambda raw, inp, **shape: (_ for _ in ()).throw(ValueError("no")))
+    monkeypatch.setattr(d, "make_runner",
+                        lambda raw, inp, **shape: (_ for _ in ()).throw(IcppCallError("icpp_gemm", -3, "no")))
     with pytest.raises(RuntimeError, match="every measured candidate failed"):
         tune(d, MI355X, top_k=2, **SHAPE)
+
+
+def test_operand_error_is_not_taken_for_a_rejected_candidate(monkeypatch, fake_device):
+    """An argument-check error (ValueError: wrong device, shape, contiguity) is a bug of
+    the caller, not a property of one tile: it propagates from the first candidate
+    instead of being recorded as a failed configuration."""
+    d = fake_device
+    calls = []
+
+    def runner(raw, inp, **shape):
+        calls.append(raw)
+        raise ValueError("A must be contiguous")
+
+    monkeypatch.setattr(d, "make_runner", runner)
+    with pytest.raises(ValueError, match="contiguous"):
+        tune(d, MI355X, top_k=4, **SHAPE)
+    assert len(calls) == 1
 
 
 def test_given_ranking_replaces_the_formula(fake_device):
