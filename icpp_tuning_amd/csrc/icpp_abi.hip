@@ -388,12 +388,12 @@ int icpp_conv2d_nhwc_fused(int inst, const void* X, const void* Wt, void* Y, con
   a.ce.residual = residual;
   hipStream_t s = (hipStream_t)stream;
   // A loader: the input halo (3x3, stride 1, pad 1, one K tile per tap, no split and the
-  // tile's halo -- its output rows spanned plus a one-row border, W+2 columns, 128 B
-  // per pixel -- within the instance's halo capacity); else the per-tile-tap gather when every K
-  // tile lies inside one tap; else the per-chunk gather
+  // tile's halo -- its output rows spanned plus a one-row border, W pixels each, and
+  // one zero pixel, 128 B per pixel -- within the instance's halo capacity); else the
+  // per-tile-tap gather when every K tile lies inside one tap; else the per-chunk gather
   const long long halo_rows = (t.block_m - 1) / W + 2 + 2;  // rows a tile can span, plus the border
   const bool halo = in->launch_halo && KH == 3 && KW == 3 && stride == 1 && dilation == 1 && pad == 1 &&
-                    C == t.block_k && a.splits == 1 && halo_rows * (W + 2) * 128 <= in->halo_bytes;
+                    C == t.block_k && a.splits == 1 && (halo_rows * W + 1) * 128 <= in->halo_bytes;
   const LaunchFn launch = halo ? in->launch_halo
                                : (C % t.block_k == 0 && KH * KW <= 32) ? in->launch : in->launch_gather;
   const dim3 grid(a.tiles_m * a.tiles_n * a.splits);  // one workgroup per (tile, K split) item

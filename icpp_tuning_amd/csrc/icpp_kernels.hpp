@@ -680,20 +680,33 @@ gemm_kernel(KArgs p) {
   // ---- A_HALO: the tile's input halo in LDS ----------------------------------
   // Output pixel m = (g, ow) with g = m / W the output row over all images
   // (stride 1, pad 1, 3x3: OH = H, OW = W).  The tile's rows g0 .. gl need input
-  // rows g0-1 .. gl+1 of the images stacked on top of each other, W+2 columns
-  // (zero border), 64 channels = eight 16-byte chunks per pixel.  Halo pixel q
-  // = (row - (g0 - 1)) * (W + 2) + column keeps chunk c at slot c ^ ((q >> 1) & 7),
-  // so 16 consecutive pixels read by one ds_read_b128 lane group hit distinct
-  // banks.  A tap (kh, kw) of output pixel (g, ow) reads halo pixel
-  // (g - g0 + kh) * (W + 2) + ow + kw; a tap whose input row lies in another
-  // image (oh + kh - 1 outside [0, H)) is masked to zero.
+  // rows g0-1 .. gl+1 of the images stacked on top of each other, 64 channels =
+  // eight 16-byte chunks per pixel: halo pixel q = (row - (g0 - 1)) * W + column,
+  // then one zero pixel Z after the last row.  A tap (kh, kw) of output pixel
+  // (g, ow) reads halo pixel (g - g0 + kh) * W + ow + kw - 1, or Z when its input
+  // column or row lies outside the image.  Without zero border columns, consecutive
+  // output pixels read consecutive halo pixels also across image rows, so the
+  // chunk swizzle c ^ ((q >> 1) & 7) keeps its pattern where an MFMA row band
+  // straddles an image row (with the border columns of an earlier layout, the
+  // pixel index jumped by 3 there: 24.6% and 39.2% LDS bank conflicts on the
+  // 256 x 64 (32x32 MFMA) and 224 x 64 (16x16) tiles at 56 x 56 x 64, 17.0% and
+  // 37.8% with this layout).  The K tiles are the 9 taps.
   constexpr int HL = HALO ? (HALO_CAP / 16 + G::THREADS - 1) / G::THREADS : 1;  // halo loads per thread
   int h_q[HALO ? G::TM : 1];       // halo pixel of this lane's row of MFMA tile tm at tap (0, 0)
-  int h_vmask[HALO ? G::TM : 1];   // bit kh: tap row kh lies inside the image
+  int h_vmask[HALO ? G::TM : 1];   // bit kh * 3 + kw: tap (kh, kw) reads inside the image
+  int h_z = 0;                     // the zero pixel Z
+  auto halo_swz = [&](int q) ICPP_INLINE { return (q >> 1) & 7; };
+  // the halo rows of item it: first output row g0 and the number of halo rows
+  auto halo_rows = [&](const Item& it, int& g0, int& rows) ICPP_INLINE {
+    g0 = it.row0 / p.cW;
+    rows = (min(it.row0 + BM, p.M) - 1) / p.cW - g0 + 3;
+  };
   auto setup_halo = [&](const Item& it) ICPP_INLINE {
     if constexpr (HALO) {
-      const int Wd = p.cW, Wp = p.cW + 2;
-      const int g0 = it.row0 / Wd;
+      const int Wd = p.cW;
+      int g0, rows;
+      halo_rows(it, g0, rows);
+      h_z = __builtin_amdgcn_readfirstlane(rows * Wd);
 #pragma unroll
       for (int tm = 0; tm < G::TM; ++tm) {
         int m = it.row0 + wm * G::WTM + tm * MF + (lane % MF);
@@ -701,29 +714,31 @@ gemm_kernel(KArgs p) {
         const int g = fdiv(m, p.dv_w);
         const int ow = m - g * Wd;
         const int oh = g - fdiv(g, p.dv_h) * p.cH;
-        h_q[tm] = (g - g0) * Wp + ow;
-        h_vmask[tm] = (oh > 0 ? 1 : 0) | 2 | (oh < p.cH - 1 ? 4 : 0);
+        h_q[tm] = (g - g0) * Wd + ow - 1;
+        const int rm = (oh > 0 ? 1 : 0) | 2 | (oh < p.cH - 1 ? 4 : 0);      // tap rows kh inside the image
+        const int cm = (ow > 0 ? 1 : 0) | 2 | (ow < Wd - 1 ? 4 : 0);        // tap columns kw inside
+        h_vmask[tm] = ((rm & 1) ? cm : 0) | ((rm & 2) ? cm << 3 : 0) | ((rm & 4) ? cm << 6 : 0);
       }
     }
   };
   auto issue_halo = [&](const Item& it) ICPP_INLINE {
     if constexpr (HALO) {
-      const int Wd = p.cW, Wp = p.cW + 2;
-      const int g0 = it.row0 / Wd;
-      const int gl = (min(it.row0 + BM, p.M) - 1) / Wd;
-      const int nslots = (gl - g0 + 3) * Wp * 8;   // the launcher keeps nslots * 16 <= HALO_CAP
-      const int rows_all = p.M / Wd;               // N * H input rows
+      const int Wd = p.cW;
+      int g0, rows;
+      halo_rows(it, g0, rows);
+      const int zpix = rows * Wd;
+      const int nslots = (zpix + 1) * 8;             // the launcher keeps nslots * 16 <= HALO_CAP
+      const int rows_all = p.M / Wd;                 // N * H input rows
 #pragma unroll
       for (int i = 0; i < HL; ++i) {
         const int s = i * G::THREADS + tid;
         if (s < nslots) {
           const int q = s >> 3;
-          const int hr = fdiv(q, p.dv_wp);
-          const int hc = q - hr * Wp;
+          const int hr = fdiv(q, p.dv_w);
           const int grow = g0 - 1 + hr;
-          const int iw = hc - 1;
-          const int chunk = (s & 7) ^ ((q >> 1) & 7);
-          const bool ok = grow >= 0 && grow < rows_all && iw >= 0 && iw < Wd;
+          const int iw = q - hr * Wd;
+          const int chunk = (s & 7) ^ halo_swz(q);
+          const bool ok = q < zpix && grow >= 0 && grow < rows_all;
           const uint32_t off = ok ? (uint32_t)(((grow * Wd + iw) * p.cC + chunk * 8) * ESZ) : p.a_bytes_total;
           dma16(ra, off, 0u, (char ICPP_LDS*)halo_lds + i * G::THREADS * 16 + wave_slot);
         }
@@ -895,19 +910,22 @@ gemm_kernel(KArgs p) {
   auto load_frags = [&](const char ICPP_LDS* as, const char ICPP_LDS* bs, auto KS, Frag* af, Frag* bf,
                         int tap) ICPP_INLINE {
     constexpr int ks = decltype(KS)::value;
-    // A_HALO: tap (kh, kw) offsets the halo pixel; K chunk of this lane's slice
-    const int t_kh = HALO ? tap / 3 : 0;
-    const int t_off = HALO ? t_kh * (p.cW + 2) + (tap - t_kh * 3) : 0;
+    // A_HALO: K tile `tap` of the tile is filter tap (kh, kw), which offsets the halo
+    // pixel.  Per MFMA row band, pa = q * 128 + ((lane K chunk ^ swizzle(q)) << 4) is the
+    // same for every K-step of the tile (computed once per tile); a K-step's first
+    // chunk only XORs bits 4-6.
+    const int t_tap = HALO ? tap : 0;
+    const int t_kh = HALO ? t_tap / 3 : 0;
+    const int t_off = HALO ? t_kh * p.cW + (t_tap - t_kh * 3) : 0;
     constexpr int h_chunk = (ks * G::KI) / 8;  // first 16-byte chunk of this K step
 #pragma unroll
     for (int tm = 0; tm < G::TM; ++tm) {
       const uint32_t row_off = (uint32_t)(tm * MF * G::ROWB_A);
       if constexpr (HALO) {
-        const int q = h_q[tm] + t_off;
-        const int c = (h_chunk + a_kgrp) ^ ((q >> 1) & 7);
-        const i32x4 v = lds_load16((const char ICPP_LDS*)halo_lds, (uint32_t)(q * 128 + c * 16));
-        const bool ok = (h_vmask[tm] >> t_kh) & 1;
-        af[tm] = ok ? v : i32x4{0, 0, 0, 0};
+        const int q = ((h_vmask[tm] >> t_tap) & 1) ? h_q[tm] + t_off : h_z;
+        const uint32_t pa = ((uint32_t)q << 7) + (uint32_t)((a_kgrp ^ halo_swz(q)) << 4);
+        // this K-step's first chunk has the lane chunk bits clear: an XOR of bits 4-6
+        af[tm] = lds_load16((const char ICPP_LDS*)halo_lds, pa ^ (uint32_t)(h_chunk << 4));
       } else if constexpr (ESZ == 2) {
         af[tm] = lds_load16(as, a_addr[tm % AP][ks][0] + row_off);
       } else {
