@@ -297,6 +297,11 @@ def tune(descriptor: TileLangKernelBase, hw: Optional[GPUSpec] = None, top_k: in
         spent_ms += ms * launches
         cands.append({"config": raw, "formatted": formatted, "score": score, "ms": ms,
                       "tflops": flops / ms / 1e9, "seed": seed})
+        # only the two fastest are timed again: release the other runners (each holds its
+        # split-K workspace; a whole-set search kept them all and ran the device out of memory)
+        keep = {c["formatted"] for c in sorted(cands, key=lambda c: c["ms"])[:2]}
+        for f in [f for f in runners if f not in keep]:
+            del runners[f]
 
     seeds = [c for c in seed_configs if c in all_cfgs]
     for c in seeds:

@@ -183,6 +183,8 @@ def _fp8_tiles() -> List[Inst]:
         _g(d, 32, 128, 256, 1, 4, 16, st=3),
         _g(d, 16, 256, 128, 1, 4, 16, st=4),
         _g(d, 16, 128, 512, 1, 4, 16),
+        _g(d, 16, 128, 128, 1, 4, 16, st=4),
+        _g(d, 16, 128, 256, 1, 4, 16, st=3),
     ]
 
 

@@ -95,3 +95,17 @@ def test_sample_shapes():
     ms = sorted({s["M"] for s in shapes})
     assert ms[:16] == list(range(1, 17)) and ms[-1] == 4096
     assert len(ss.generate_conv2d_sample_shapes()) == 6 * 6 * 4 * 4
+
+
+def test_tiles_of_8x_the_rows_are_not_offered():
+    """A tile of 8x or more the problem's rows (rounded to 16) is not offered while a
+    shorter one is: at M = 16 no 128- or 256-row tile, at M = 40 (48 rows) none of 384+."""
+    from icpp_tuning_amd.kernels import fp8_gemm_bias_act as F
+
+    d = F.DESCRIPTOR
+    rows16 = {c["block_M"] for c in d.get_raw_configs(M=16, N=4096, K=4096)}
+    assert rows16 and max(rows16) < 128 and 16 in rows16
+    rows40 = {c["block_M"] for c in d.get_raw_configs(M=40, N=4096, K=4096)}
+    assert 256 in rows40
+    rows4k = {c["block_M"] for c in d.get_raw_configs(M=4096, N=4096, K=4096)}
+    assert rows4k == {i.bm for i in d.instances()}
