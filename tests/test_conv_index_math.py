@@ -70,3 +70,63 @@ def test_tap_mask_closed_form_matches_loop(KH, KW):
                 for iw0 in range(-KW - 1, W + 2):
                     assert tap_mask_closed(ih0, iw0, H, W, KH, KW) == tap_mask_loop(ih0, iw0, H, W, KH, KW), \
                         (ih0, iw0, H, W, KH, KW)
+
+
+def _halo_tile(Nb, H, W, BM, MF, row0, wave_rows):
+    """The A_HALO tile of 64 channels starting at output row row0, as the kernel lays it out
+    (icpp_kernels.hpp setup_halo / issue_halo / load_frags): the LDS image the loader writes
+    -- {slot: (n, h, w, logical chunk) or None for zeros} -- and, per (output pixel, tap,
+    lane K chunk), the LDS slot the fragment read takes."""
+    M = Nb * H * W
+    g0 = row0 // W
+    rows = (min(row0 + BM, M) - 1) // W - g0 + 3
+    zpix = rows * W
+    rows_all = M // W
+    swz = lambda q: (q >> 1) & 7
+    lds = {}
+    for s in range((zpix + 1) * 8):                 # issue_halo
+        q = s >> 3
+        hr, iw = divmod(q, W)
+        grow = g0 - 1 + hr
+        chunk = (s & 7) ^ swz(q)
+        ok = q < zpix and 0 <= grow < rows_all
+        lds[s] = (grow // H, grow % H, iw, chunk) if ok else None
+    reads = {}
+    for r in range(wave_rows):                      # setup_halo + load_frags, one lane row each
+        m = min(row0 + r, M - 1)
+        g, ow = divmod(m, W)
+        oh = g % H
+        hq = (g - g0) * W + ow - 1
+        rm = (oh > 0) | 2 | ((oh < H - 1) << 2)
+        cm = (ow > 0) | 2 | ((ow < W - 1) << 2)
+        vmask = (cm if rm & 1 else 0) | ((cm << 3) if rm & 2 else 0) | ((cm << 6) if rm & 4 else 0)
+        for tap in range(9):
+            kh, kw = divmod(tap, 3)
+            q = hq + kh * W + kw if (vmask >> tap) & 1 else zpix
+            for kgrp in range(4 if MF == 16 else 2):   # lane K chunk within a K-step
+                for h_chunk in ((0, 4) if MF == 16 else (0, 2, 4, 6)):
+                    pa = (q << 7) + ((kgrp ^ swz(q)) << 4)
+                    off = pa ^ (h_chunk << 4)
+                    reads[(r, tap, h_chunk + kgrp)] = (m, off // 16)
+    return lds, reads
+
+
+@pytest.mark.parametrize("geo", [(3, 9, 11, 256, 16), (2, 13, 5, 256, 16), (1, 56, 56, 256, 32), (4, 7, 7, 64, 16),
+                                 (2, 6, 14, 224, 16)])
+def test_halo_reads_fetch_the_tap_input_or_zero(geo):
+    """Every (output pixel, tap, 16-byte K chunk) the fragment reads of an A_HALO tile take
+    from LDS holds input pixel (n, oh + kh - 1, ow + kw - 1), channels 8 * chunk .. + 7, or
+    zeros when that pixel lies outside the image -- checked against the definition of the
+    3x3 stride-1 pad-1 conv for every tile of the shape (brute force over the loader's LDS
+    image)."""
+    Nb, H, W, BM, MF = geo
+    M = Nb * H * W
+    for row0 in range(0, M, BM):
+        lds, reads = _halo_tile(Nb, H, W, BM, MF, row0, min(BM, M - row0))
+        for (r, tap, chunk), (m, slot) in reads.items():
+            n, rem = divmod(m, H * W)
+            oh, ow = divmod(rem, W)
+            kh, kw = divmod(tap, 3)
+            ih, iw = oh + kh - 1, ow + kw - 1
+            want = (n, ih, iw, chunk) if 0 <= ih < H and 0 <= iw < W else None
+            assert lds[slot] == want, (geo, row0, r, tap, chunk)

@@ -345,6 +345,12 @@ def test_conv_every_instance_full_size(gpu, shape, sk):
     (2, 9, 9, 64, 64, 3, 3, 2, 1, 1),    # stride 2
     (2, 8, 8, 64, 128, 3, 3, 1, 2, 2),   # dilation 2
     (1, 5, 5, 128, 72, 1, 1, 1, 0, 1),   # 1x1, F not a multiple of the tile
+    # input halo (3x3 stride 1 pad 1, C = 64): MFMA row bands that straddle image rows
+    # and images, taps outside the image redirected to the zero pixel
+    (3, 9, 11, 64, 72, 3, 3, 1, 1, 1),   # W = 11, F not a multiple of the tile
+    (2, 13, 5, 64, 64, 3, 3, 1, 1, 1),   # W = 5: a 256-row tile spans both images
+    (1, 56, 56, 64, 64, 3, 3, 1, 1, 1),  # one image, the widest the halo holds
+    (2, 6, 80, 64, 64, 3, 3, 1, 1, 1),   # W = 80: past the halo capacity of every tile, the gathers take it
 ])
 def test_conv_geometries(gpu, geom):
     Nb, H, W, C, F, KH, KW, S, P, D = geom
