@@ -728,18 +728,18 @@ gemm_kernel(KArgs p) {
       halo_rows(it, g0, rows);
       const int zpix = rows * Wd;
       const int nslots = (zpix + 1) * 8;             // the launcher keeps nslots * 16 <= HALO_CAP
-      const int rows_all = p.M / Wd;                 // N * H input rows
+      // halo pixel q is input pixel (g0 - 1) * W + q of the N*H*W stacked pixels (rows
+      // past the first or last image row of the batch load zeros)
+      const int pix0 = (g0 - 1) * Wd;
 #pragma unroll
       for (int i = 0; i < HL; ++i) {
         const int s = i * G::THREADS + tid;
         if (s < nslots) {
           const int q = s >> 3;
-          const int hr = fdiv(q, p.dv_w);
-          const int grow = g0 - 1 + hr;
-          const int iw = q - hr * Wd;
+          const int pix = pix0 + q;
           const int chunk = (s & 7) ^ halo_swz(q);
-          const bool ok = q < zpix && grow >= 0 && grow < rows_all;
-          const uint32_t off = ok ? (uint32_t)(((grow * Wd + iw) * p.cC + chunk * 8) * ESZ) : p.a_bytes_total;
+          const bool ok = q < zpix && pix >= 0 && pix < p.M;
+          const uint32_t off = ok ? (uint32_t)((pix * p.cC + chunk * 8) * ESZ) : p.a_bytes_total;
           dma16(ra, off, 0u, (char ICPP_LDS*)halo_lds + i * G::THREADS * 16 + wave_slot);
         }
       }

@@ -81,16 +81,14 @@ def _halo_tile(Nb, H, W, BM, MF, row0, wave_rows):
     g0 = row0 // W
     rows = (min(row0 + BM, M) - 1) // W - g0 + 3
     zpix = rows * W
-    rows_all = M // W
     swz = lambda q: (q >> 1) & 7
     lds = {}
     for s in range((zpix + 1) * 8):                 # issue_halo
         q = s >> 3
-        hr, iw = divmod(q, W)
-        grow = g0 - 1 + hr
+        pix = (g0 - 1) * W + q
         chunk = (s & 7) ^ swz(q)
-        ok = q < zpix and 0 <= grow < rows_all
-        lds[s] = (grow // H, grow % H, iw, chunk) if ok else None
+        ok = q < zpix and 0 <= pix < M
+        lds[s] = (pix // (H * W), pix % (H * W) // W, pix % W, chunk) if ok else None
     reads = {}
     for r in range(wave_rows):                      # setup_halo + load_frags, one lane row each
         m = min(row0 + r, M - 1)
