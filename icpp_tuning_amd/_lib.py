@@ -20,6 +20,10 @@ RESOURCES_PATH = PKG / "libicpp_hip.resources.json"
 ABI_VERSION = 2
 FAMILY = {"gemm": 0, "gemm_ln_stats": 1, "gemm_ln_row": 2, "conv2d": 3}
 FAMILY_NAME = {v: k for k, v in FAMILY.items()}
+# strategy codes of the LayerNorm entry points: the instance families above plus
+# ICPP_LN_CORESIDENT (f16 GEMM instances run with the co-resident row-block epilogue)
+LN_CORESIDENT = 16
+LN_STRATEGY = dict(FAMILY, gemm_ln_cr=LN_CORESIDENT)
 DTYPE = {"f16": 0, "bf16": 1, "fp8": 2, "f32": 3}
 DTYPE_NAME = {v: k for k, v in DTYPE.items()}
 ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu": 2, "silu": 3, "gelu_erf": 4}
@@ -178,4 +182,4 @@ def resources() -> Dict[str, dict]:
     return _resources_cache["data"]
 
 
-__all__ = ["ACT", "DTYPE", "EXPORTED_SYMBOLS", "FAMILY", "IcppCallError", "IcppLibraryError", "Lib", "lib", "resources"]
+__all__ = ["ACT", "DTYPE", "EXPORTED_SYMBOLS", "FAMILY", "LN_CORESIDENT", "LN_STRATEGY", "IcppCallError", "IcppLibraryError", "Lib", "lib", "resources"]

@@ -66,6 +66,30 @@ int check_launch(hipError_t e, const char* what) {
   return ICPP_OK;
 }
 
+// Workspace of the co-resident LayerNorm: per-(row, tile column) (mean, M2) pairs, a
+// 16-byte block whose first int flags a wait that ran out, then the [tiles_m][2]
+// arrival / departure counters.
+struct LnCrLayout { size_t err_off, ctr_off, bytes; };
+LnCrLayout ln_cr_layout(const icpp_tile_t& t, int M, int N) {
+  LnCrLayout l;
+  const size_t stats = (size_t)M * ceil_div(N, t.block_n) * 2 * sizeof(float);
+  l.err_off = (stats + 15) / 16 * 16;
+  l.ctr_off = l.err_off + 16;
+  l.bytes = l.ctr_off + (size_t)ceil_div(M, t.block_m) * 2 * sizeof(int);
+  return l;
+}
+
+// Workgroups of an instance's co-resident LayerNorm kernel the current device holds at
+// once: CUs x workgroups per CU (the occupancy query, capped by the LDS a CU has).
+int ln_cr_capacity(const Instance* in) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  int per_cu = in->resident_ln_cr ? in->resident_ln_cr() : 0;
+  per_cu = std::min(per_cu, (160 * 1024) / std::max(1, in->tile.lds_bytes));
+  return std::max(0, cus) * std::max(0, per_cu);
+}
+
 hipError_t launch_splitk_reduce(int dt, const float* ws, void* C, const void* bias, int M, int N, int ldc,
                                 int splits, float alpha, int act, hipStream_t s, ConvEpiArgs ce = ConvEpiArgs{}) {
   const size_t groups = (size_t)M * (N / 4);
@@ -229,6 +253,12 @@ size_t icpp_gemm_bias_layernorm_workspace_bytes(int family, int inst, int M, int
     return (size_t)M * ceil_div(N, in->wave_tile_n) * sizeof(float);
   }
   if (family == ICPP_FAMILY_GEMM_LN_STATS) return icpp_workspace_bytes(family, inst, M, N, K, 1);
+  if (family == ICPP_LN_CORESIDENT) {
+    const Instance* in = lookup(ICPP_FAMILY_GEMM, inst);
+    if (!in || !in->launch_ln_cr) return 0;
+    const LnCrLayout l = ln_cr_layout(in->tile, M, N);
+    return l.bytes;
+  }
   return 0;
 }
 
@@ -244,6 +274,56 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
                                       const void* residual, const void* gamma, const void* beta, void* Y,
                                       int M, int N, int K, float eps,
                                       void* workspace, size_t ws_bytes, void* stream) {
+  if (family == ICPP_LN_CORESIDENT) {
+    // One launch per chunk of row blocks that the device keeps resident at once; the
+    // tiles of a row block exchange their (mean, M2) and normalise from registers.
+    if (!gamma || !beta) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: null tensor");
+    const Instance* gi = lookup(ICPP_FAMILY_GEMM, inst);
+    if (!gi) return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: no GEMM instance %d", inst);
+    if (gi->tile.dtype != DT_F16 || !gi->launch_ln_cr)
+      return fail(ICPP_E_INSTANCE, "icpp_gemm_bias_layernorm: GEMM instance %s has no co-resident LayerNorm kernel",
+                  gi->tile.name);
+    if (!(eps > 0.f)) return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: eps must be > 0");
+    if ((residual && !aligned16(residual)) || !aligned16(gamma) || !aligned16(beta))
+      return fail(ICPP_E_ARG, "icpp_gemm_bias_layernorm: pointers must be 16-byte aligned");
+    KArgs a;
+    if (int rc = gemm_prepare("icpp_gemm_bias_layernorm", inst, A, B, bias, Y, M, N, K, K, N, N, ICPP_ACT_NONE, 1.f,
+                              1.f, 1, &gi, &a))
+      return rc;
+    const icpp_tile_t& t = gi->tile;
+    if ((size_t)t.block_m * a.tiles_n * 2 * sizeof(float) > (size_t)gi->ln_cr_stage_bytes)
+      return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: N=%d is too wide for %s: a row block's statistics exceed one LDS stage",
+                  N, t.name);
+    const int cap = ln_cr_capacity(gi);
+    if (cap < a.tiles_n)
+      return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: %s: the %d tiles of a row block cannot be resident at once (%d)",
+                  t.name, a.tiles_n, cap);
+    const LnCrLayout l = ln_cr_layout(t, M, N);
+    if (!workspace || ws_bytes < l.bytes || !aligned16(workspace))
+      return fail(ICPP_E_WORKSPACE, "icpp_gemm_bias_layernorm: needs %zu workspace bytes (got %zu)", l.bytes, ws_bytes);
+    a.gamma = gamma; a.beta = beta; a.eps = eps; a.residual = residual;
+    char* w = (char*)workspace;
+    int* ctr = (int*)(w + l.ctr_off);
+    a.ln_err = (int*)(w + l.err_off);
+    // even chunks of at most cap / tiles_n row blocks
+    const int max_rows = cap / a.tiles_n;
+    const int chunks = ceil_div(a.tiles_m, max_rows);
+    const int chunk_tm = ceil_div(a.tiles_m, chunks);
+    hipStream_t s = (hipStream_t)stream;
+    for (int tm0 = 0; tm0 < a.tiles_m; tm0 += chunk_tm) {
+      const int r0 = tm0 * t.block_m;
+      KArgs b = a;
+      b.A = (const char*)A + (size_t)r0 * K * 2;
+      b.C = (char*)Y + (size_t)r0 * N * 2;
+      if (residual) b.residual = (const char*)residual + (size_t)r0 * N * 2;
+      b.M = std::min(M - r0, chunk_tm * t.block_m);
+      b.tiles_m = ceil_div(b.M, t.block_m);
+      b.ws = (float*)w + (size_t)r0 * a.tiles_n * 2;
+      b.ln_ctr = ctr + 2 * tm0;
+      if (int rc = check_launch(gi->launch_ln_cr(b, dim3(b.tiles_m * b.tiles_n), s), t.name)) return rc;
+    }
+    return ICPP_OK;
+  }
   if (family == ICPP_FAMILY_GEMM) {
     // GEMM-then-LayerNorm: a plain f16 GEMM + bias into Y (staged epilogue, any GEMM tile), then
     // the row LayerNorm kernel in place (adding the residual); the same HBM traffic as two-pass

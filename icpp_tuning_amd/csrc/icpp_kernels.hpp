@@ -38,7 +38,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 enum DType { DT_F16 = 0, DT_BF16 = 1, DT_FP8 = 2, DT_F32 = 3 };
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2, ACT_SILU = 3, ACT_GELU_ERF = 4 };
-enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2 };
+enum Epi { EPI_STORE = 0, EPI_LN_STATS = 1, EPI_LN_ROW = 2, EPI_LN_CR = 3 };
 // A operand loaders: dense rows, the NHWC implicit-GEMM gather for any C
 // (per 16-byte chunk), the gather for C % BK == 0, where every K tile is one
 // filter tap so the tap decomposition is per tile rather than per chunk, and the
@@ -114,6 +114,8 @@ struct KArgs {
   uint32_t a_bytes_total;  // X size in bytes (buffer range for the gather)
   ConvEpiArgs ce;          // fused conv epilogue (conv instances only)
   const void* residual;    // LayerNorm epilogues: [M, ldc] (output type) added before the statistics, or null
+  int* ln_ctr;             // EPI_LN_CR: [tiles_m][2] arrival / departure counters (zero between calls)
+  int* ln_err;             // EPI_LN_CR: set to 1 when a row block's wait ran out
 };
 
 template <int DT> struct DTraits;
@@ -322,6 +324,40 @@ template <> struct Vec4Store<float> {
   static __device__ __forceinline__ void st_lds(char ICPP_LDS* p, f32x4 v) { *reinterpret_cast<f32x4 ICPP_LDS*>(p) = v; }
   static __device__ __forceinline__ f32x4 ld(const void* p) { return *reinterpret_cast<const f32x4*>(p); }
   static __device__ __forceinline__ f32x4 ld_lds(const char ICPP_LDS* p) { return *reinterpret_cast<const f32x4 ICPP_LDS*>(p); }
+};
+
+// Four consecutive elements of a vector through a range-checked buffer descriptor:
+// past the range the hardware returns zeros, so the loads of an epilogue need no
+// branch around them and all go out before one wait (a branch per load makes the
+// compiler wait for each one in turn).  vec_rsrc covers len elements, or none for a
+// null vector.  Rows are padded so that a group of 4 never straddles the end (N % 8
+// == 0).  The raw result is reinterpreted as a whole vector.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t vec_rsrc(const void* p, int len) {
+  return make_rsrc(p, p ? (uint32_t)len * (uint32_t)sizeof(T) : 0u);
+}
+template <typename T> struct Vec4Ld;
+template <> struct Vec4Ld<_Float16> {
+  static __device__ __forceinline__ f32x4 at(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  }
+  static __device__ __forceinline__ f32x4 ld(__amdgpu_buffer_rsrc_t r, int n) { return at(r, (uint32_t)n * 2u); }
+};
+template <> struct Vec4Ld<__bf16> {
+  static __device__ __forceinline__ f32x4 at(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    const b4 h = __builtin_bit_cast(b4, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, 0));
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  }
+  static __device__ __forceinline__ f32x4 ld(__amdgpu_buffer_rsrc_t r, int n) { return at(r, (uint32_t)n * 2u); }
+};
+template <> struct Vec4Ld<float> {
+  static __device__ __forceinline__ f32x4 at(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+  }
+  static __device__ __forceinline__ f32x4 ld(__amdgpu_buffer_rsrc_t r, int n) { return at(r, (uint32_t)n * 4u); }
 };
 
 // Per-channel BN of columns n..n+3 for the fused conv epilogue, folded to
@@ -1186,15 +1222,12 @@ gemm_kernel(KArgs p) {
           else run(std::false_type{});
         }
       } else {
-        const BiasT* bias = (const BiasT*)p.bias;
+        const __amdgpu_buffer_rsrc_t bias_r = vec_rsrc<BiasT>(p.bias, p.N);
         f32x4 bv[G::TN][NG];
 #pragma unroll
         for (int tn = 0; tn < G::TN; ++tn)
 #pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const int n = out_col(tn, g);
-            bv[tn][g] = (bias != nullptr && n < p.N) ? Vec4Store<BiasT>::ld(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
-          }
+          for (int g = 0; g < NG; ++g) bv[tn][g] = Vec4Ld<BiasT>::ld(bias_r, out_col(tn, g));
         // LayerNorm producer (p.stat_cols > 0, act none): each row's values over this
         // wave's WTN columns are stored minus their mean, and the mean goes to
         // ws[m * stat_cols + column block] in fp32.  The LayerNorm pass adds it back,
@@ -1237,7 +1270,7 @@ gemm_kernel(KArgs p) {
     } else {
       // LayerNorm epilogues: x = acc + bias (+ residual), statistics over valid columns (n < N)
       OutT* C = (OutT*)p.C;
-      const BiasT* bias = (const BiasT*)p.bias;
+      const __amdgpu_buffer_rsrc_t bias_r = vec_rsrc<BiasT>(p.bias, p.N);
       const OutT* res = (const OutT*)p.residual;
       float xs[G::TM][G::TN][Op::ACC];
 #pragma unroll
@@ -1245,8 +1278,7 @@ gemm_kernel(KArgs p) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           const int n = out_col(tn, g);
-          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-          if (bias != nullptr && n < p.N) bv = Vec4Store<BiasT>::ld(bias + n);
+          const f32x4 bv = Vec4Ld<BiasT>::ld(bias_r, n);
           const bool ok = n < p.N;
 #pragma unroll
           for (int tm = 0; tm < G::TM; ++tm)
@@ -1255,20 +1287,23 @@ gemm_kernel(KArgs p) {
         }
       if (res != nullptr) {
         // one row band's loads at a time (a scheduling barrier per band): the largest
-        // tiles have no registers left for every band's residual in flight
+        // tiles have no registers left for every band's residual in flight.  Rows past M
+        // and columns past N read zeros from the descriptor over the tile's rows.
+        const uint32_t res_rows = (uint32_t)(p.M > row0 ? min(p.M - row0, BM) : 0);
+        const __amdgpu_buffer_rsrc_t res_r =
+            make_rsrc(res + (size_t)row0 * p.ldc, res_rows * (uint32_t)p.ldc * (uint32_t)sizeof(OutT));
 #pragma unroll
         for (int tm = 0; tm < G::TM; ++tm) {
-          const int m = out_row(tm);
+          const int r = out_row(tm) - row0;
 #pragma unroll
           for (int tn = 0; tn < G::TN; ++tn)
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
               const int n = out_col(tn, g);
-              if (n < p.N && m < p.M) {
-                const f32x4 rv = Vec4Store<OutT>::ld(res + (size_t)m * p.ldc + n);
+              const uint32_t off = n < p.N ? (uint32_t)(r * p.ldc + n) * (uint32_t)sizeof(OutT) : ICPP_OOB_OFFSET;
+              const f32x4 rv = Vec4Ld<OutT>::at(res_r, off);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] += rv[e];
-              }
+              for (int e = 0; e < 4; ++e) xs[tm][tn][4 * g + e] += rv[e];
             }
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -1317,15 +1352,15 @@ gemm_kernel(KArgs p) {
               if (m < p.M && n < p.N) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
             }
         }
-      } else {
+      } else if constexpr (EPI == EPI_LN_ROW) {
         // EPI_LN_ROW: the workgroup owns whole rows (tiles_n == 1, N <= BN); two-pass
         // mean / centred variance in registers, cross-wave through LDS.
         __syncthreads();  // mainloop LDS no longer needed
         static_assert(2 * WN * BM * 4 <= SBYTES, "LN reduction scratch must fit one LDS stage");
         float ICPP_LDS* red = (float ICPP_LDS*)lds0;       // [WN][BM]
         float ICPP_LDS* red2 = red + WN * BM;               // [WN][BM]
-        const BiasT* gamma = (const BiasT*)p.gamma;
-        const BiasT* beta = (const BiasT*)p.beta;
+        const __amdgpu_buffer_rsrc_t gamma_r = vec_rsrc<BiasT>(p.gamma, p.N);
+        const __amdgpu_buffer_rsrc_t beta_r = vec_rsrc<BiasT>(p.beta, p.N);
         const float inv_n = 1.f / (float)p.N;
         float mean[G::TM], rstd[G::TM];
 #pragma unroll
@@ -1375,9 +1410,9 @@ gemm_kernel(KArgs p) {
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
             const int n = out_col(tn, g);
+            const f32x4 gv = Vec4Ld<BiasT>::ld(gamma_r, n);
+            const f32x4 bv = Vec4Ld<BiasT>::ld(beta_r, n);
             if (n >= p.N) continue;
-            const f32x4 gv = Vec4Store<BiasT>::ld(gamma + n);
-            const f32x4 bv = Vec4Store<BiasT>::ld(beta + n);
 #pragma unroll
             for (int tm = 0; tm < G::TM; ++tm) {
               const int m = out_row(tm);
@@ -1387,6 +1422,164 @@ gemm_kernel(KArgs p) {
               if (m < p.M) Vec4Store<OutT>::st(C + (size_t)m * p.ldc + n, v);
             }
           }
+      } else {
+        // EPI_LN_CR (co-resident row blocks): the launcher sizes every launch so that all
+        // of its workgroups are resident at once.  The tiles_n workgroups of a row block
+        // each publish their rows' (mean, M2) over their own columns to ws[m][tile column],
+        // count themselves in on the row block's arrival counter and wait until all
+        // tiles_n have; each then merges the row's tiles_n pairs in column order (Chan et
+        // al., so the result does not depend on arrival order) and normalises its tile
+        // from registers.  X never goes to memory and there is no second pass.
+        // ln_ctr[2 rb] counts arrivals and ln_ctr[2 rb + 1] departures; the last
+        // workgroup to depart zeroes both, so a call leaves the counters zero as it found
+        // them.  A wait that runs out (workgroups not co-resident) sets *ln_err.
+        // Everything that crosses workgroups -- the pairs and the counters -- goes through
+        // device-scope stores and loads (sc1) and device atomics, which bypass the
+        // per-XCD L2s' non-coherent copies, so no L2 write-back or invalidate is needed
+        // (an agent-scope release fence here, an L2 write-back per wave, cost more than
+        // the whole second pass it removes): each wave's pair stores complete (vmcnt 0)
+        // before the barrier ahead of the arrival count, and the pair loads issue after
+        // the barrier behind the observed count.
+        static_assert(STAGES >= 2, "EPI_LN_CR keeps per-row results in the second stage array");
+        constexpr int LN_CR_SPINS = 1 << 17;  // ~0.1-0.3 s of polling before giving up
+        __syncthreads();  // every wave is done with the mainloop's LDS
+        float ICPP_LDS* red = (float ICPP_LDS*)lds0;  // [WN][BM] per-wave row sums, then M2
+        float ICPP_LDS* rowst = (float ICPP_LDS*)lds1;  // [BM][2] merged (mean, rstd)
+        const int tcnt = max(0, min(BN, p.N - col0));
+        const float inv_t = tcnt > 0 ? 1.f / (float)tcnt : 0.f;
+        float tmean[G::TM];
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          float sum = 0.f;
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int e = 0; e < Op::ACC; ++e) sum += xs[tm][tn][e];  // zero past N
+          sum = lane_reduce(sum);
+          if (lane < MF) red[wn * BM + wm * G::WTM + tm * MF + lane] = sum;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          const int lr = wm * G::WTM + tm * MF + (lane % MF);
+          float sum = 0.f;
+#pragma unroll
+          for (int w = 0; w < WN; ++w) sum += red[w * BM + lr];
+          tmean[tm] = sum * inv_t;
+        }
+        __syncthreads();  // red is reused for M2
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          float q = 0.f;
+#pragma unroll
+          for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+              const bool ok = out_col(tn, g) < p.N;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const float d = xs[tm][tn][4 * g + e] - tmean[tm];
+                q += ok ? d * d : 0.f;
+              }
+            }
+          q = lane_reduce(q);
+          if (lane < MF) red[wn * BM + wm * G::WTM + tm * MF + lane] = q;
+        }
+        __syncthreads();
+        const int rb = row0 / BM, tcol = col0 / BN;
+        if (wn == 0) {
+#pragma unroll
+          for (int tm = 0; tm < G::TM; ++tm) {
+            const int lr = wm * G::WTM + tm * MF + (lane % MF);
+            float q = 0.f;
+#pragma unroll
+            for (int w = 0; w < WN; ++w) q += red[w * BM + lr];
+            const int m = out_row(tm);
+            if (lane < MF && m < p.M) {
+              float* dst = p.ws + ((size_t)m * p.tiles_n + tcol) * 2;
+              __hip_atomic_store(dst, tmean[tm], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              __hip_atomic_store(dst + 1, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0);  // this wave's pair stores have completed
+        }
+        __syncthreads();
+        if (tid == 0) {
+          int* ctr = p.ln_ctr + 2 * rb;
+          __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          int spins = 0;
+          while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < p.tiles_n) {
+            if (++spins > LN_CR_SPINS) {
+              __hip_atomic_store(p.ln_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+          }
+          // this workgroup no longer reads the arrival counter; the last to leave resets the pair
+          if (__hip_atomic_fetch_add(ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.tiles_n - 1) {
+            __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ctr + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        __syncthreads();
+        // The row block's pairs are one contiguous [BM][tiles_n][2] block of ws: 16-byte
+        // device-scope loads spread over the workgroup bring it into LDS (the launcher
+        // checks that it fits one stage array), then one thread per row merges it.
+        {
+          float ICPP_LDS* pairs = (float ICPP_LDS*)lds0;
+          const int rows = max(0, min(BM, p.M - row0));
+          const int nvec = rows * p.tiles_n / 2;  // tiles_n pairs of 8 bytes per row; BM and rows*tiles_n even
+          const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.ws + (size_t)row0 * p.tiles_n * 2, (uint32_t)(nvec * 16));
+          for (int i = tid; i < nvec; i += G::THREADS)
+            *(i32x4 ICPP_LDS*)(pairs + 4 * i) = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(i * 16), 0, 16);
+          if ((rows * p.tiles_n) & 1) {  // an odd last pair (odd tiles_n and an odd row count)
+            if (tid == 0) {
+              const int j = rows * p.tiles_n - 1;
+              pairs[2 * j] = __hip_atomic_load(p.ws + ((size_t)row0 * p.tiles_n + j) * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              pairs[2 * j + 1] = __hip_atomic_load(p.ws + ((size_t)row0 * p.tiles_n + j) * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+          __syncthreads();
+          for (int r = tid; r < rows; r += G::THREADS) {
+            float n_acc = 0.f, mu = 0.f, m2 = 0.f;
+            for (int j = 0; j < p.tiles_n; ++j) {
+              const float nb = (float)max(0, min(BN, p.N - j * BN));
+              const float mb = pairs[(r * p.tiles_n + j) * 2 + 0];
+              const float qb = pairs[(r * p.tiles_n + j) * 2 + 1];
+              const float nt = n_acc + nb;
+              const float d = mb - mu;
+              mu += d * (nb / nt);
+              m2 += qb + d * d * (n_acc * nb / nt);
+              n_acc = nt;
+            }
+            rowst[2 * r + 0] = mu;
+            rowst[2 * r + 1] = rsqrtf(m2 / (float)p.N + p.eps);
+          }
+          __syncthreads();
+        }
+        const __amdgpu_buffer_rsrc_t gamma_r = vec_rsrc<BiasT>(p.gamma, p.N);
+        const __amdgpu_buffer_rsrc_t beta_r = vec_rsrc<BiasT>(p.beta, p.N);
+        f32x4 gv[G::TN][NG], bt[G::TN][NG];
+#pragma unroll
+        for (int tn = 0; tn < G::TN; ++tn)
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            gv[tn][g] = Vec4Ld<BiasT>::ld(gamma_r, out_col(tn, g));
+            bt[tn][g] = Vec4Ld<BiasT>::ld(beta_r, out_col(tn, g));
+          }
+        float mean[G::TM], rstd[G::TM];
+#pragma unroll
+        for (int tm = 0; tm < G::TM; ++tm) {
+          const int lr = wm * G::WTM + tm * MF + (lane % MF);
+          mean[tm] = rowst[2 * lr + 0];
+          rstd[tm] = rowst[2 * lr + 1];
+        }
+        store_staged([&](int tm, int tn, int g) ICPP_INLINE {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (xs[tm][tn][4 * g + e] - mean[tm]) * rstd[tm] * gv[tn][g][e] + bt[tn][g][e];
+          return v;
+        });
       }
     }
   };
@@ -1436,8 +1629,8 @@ gemm_kernel(KArgs p) {
     // Group g = wave / 4: waves w and w + 4 share a SIMD whatever the 8-wave grid.
     // Each wave issues the tiles in order (group 1 one tile ahead of group 0), so
     // the conv loaders take the next tile from the issue cursor.
-    static_assert(WM * WN == 8 && STAGES >= 2 && EPI == EPI_STORE,
-                  "ping-pong: 8 waves (one wave of each group per SIMD), store epilogue");
+    static_assert(WM * WN == 8 && STAGES >= 2 && (EPI == EPI_STORE || EPI == EPI_LN_CR),
+                  "ping-pong: 8 waves (one wave of each group per SIMD), a staged-store epilogue");
     // The fragments of one tile live from its memory phase to its MFMA phase of
     // the same iteration only; the accumulators are the only loop-carried state.
     auto read_tile = [&](auto J, int kt, Frag (&fa_)[NKS][G::TM], Frag (&fb_)[NKS][G::TN]) ICPP_INLINE {

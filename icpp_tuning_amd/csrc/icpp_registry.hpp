@@ -18,6 +18,12 @@ struct Instance {
   LaunchFn launch_gather;  // conv instances: the per-chunk gather (any C % 8 == 0); else null
   LaunchFn launch_halo;    // conv instances: the input-halo loader (3x3 stride 1 pad 1, C == block_k); or null
   int halo_bytes;          // its halo capacity (halo_cap(block_m))
+  // f16 dense GEMM instances: the same tile with the co-resident LayerNorm epilogue
+  // (EPI_LN_CR), its workgroups resident per CU, and the LDS bytes of one stage array
+  // (the row block's statistics are gathered into it); else null / 0
+  LaunchFn launch_ln_cr;
+  int (*resident_ln_cr)();
+  int ln_cr_stage_bytes;
 };
 
 int register_instance(const Instance& inst);
@@ -26,6 +32,17 @@ template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int ST, int EP
 hipError_t launch_instance(const KArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL((gemm_kernel<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>), grid, dim3(WM * WN * 64), 0, s, a);
   return hipGetLastError();
+}
+
+// Workgroups of the kernel one CU holds at once (registers, LDS, waves), 0 if unknown.
+template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int ST, int EPI, int AL>
+int resident_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, reinterpret_cast<const void*>(&gemm_kernel<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>), WM * WN * 64, 0) !=
+      hipSuccess)
+    return 0;
+  return n;
 }
 
 template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int ST, int EPI, int AL>
@@ -62,6 +79,15 @@ Instance make_instance(int family, const char* name) {
   } else {
     in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>;
     in.launch_gather = nullptr;
+  }
+  if constexpr (DT == DT_F16 && EPI == EPI_STORE && (AL & 7) == A_DENSE && BM >= 64 && BN >= 128 && ST >= 2) {
+    in.launch_ln_cr = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI_LN_CR, AL>;
+    in.resident_ln_cr = &resident_per_cu<DT, BM, BN, BK, WM, WN, MF, ST, EPI_LN_CR, AL>;
+    in.ln_cr_stage_bytes = G::STAGE_BYTES;
+  } else {
+    in.launch_ln_cr = nullptr;
+    in.resident_ln_cr = nullptr;
+    in.ln_cr_stage_bytes = 0;
   }
   return in;
 }

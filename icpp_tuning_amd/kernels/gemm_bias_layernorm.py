@@ -17,6 +17,11 @@ chosen per shape by the tuner:
               stores) plus per-(row, wave column block) means in the workspace,
               then the row LayerNorm kernel in place: the same HBM traffic as
               two-pass, with only a mean in the epilogue.
+  "coresident" (gemm, f16)     one launch per chunk of row blocks the device keeps
+              resident at once: the tiles of a row block exchange their rows'
+              (mean, M2) through the workspace, wait for each other, and normalise
+              from registers -- no X in memory, no second pass (the reference's
+              fp32 X never leaves the accumulators).
 
 Both two-launch strategies keep X in Y as f16 values centred on their block's
 mean (the mean itself in fp32 in the workspace), where the reference keeps X in
@@ -36,7 +41,21 @@ from .. import inputs as _inputs
 from .. import runtime
 from ._base import InstanceDescriptor, family_instances, raw_from_inst
 
-STRATEGY_FAMILY = {"row": "gemm_ln_row", "two_pass": "gemm_ln_stats", "gemm_ln": "gemm"}
+STRATEGY_FAMILY = {"row": "gemm_ln_row", "two_pass": "gemm_ln_stats", "gemm_ln": "gemm", "coresident": "gemm"}
+# the strategy code passed to the C ABI (runtime.ln_workspace_bytes / gemm_bias_layernorm)
+STRATEGY_CALL = {"row": "gemm_ln_row", "two_pass": "gemm_ln_stats", "gemm_ln": "gemm", "coresident": "gemm_ln_cr"}
+SUFFIX = {"row": "_ROW", "two_pass": "_2P", "gemm_ln": "_GL", "coresident": "_CR"}
+
+
+def coresident_fits(inst, N: int) -> bool:
+    """The f16 GEMM tiles built with the co-resident LayerNorm kernel (block_m >= 64,
+    block_n >= 128, 2+ stages), for row widths whose block_m x ceil(N / block_n)
+    (mean, M2) pairs fit one LDS stage array; the library also checks that one row
+    block's ceil(N / block_n) workgroups fit the device at once."""
+    if inst.family != "gemm" or inst.dtype != "f16" or inst.bm < 64 or inst.bn < 128 or inst.stages < 2:
+        return False
+    stage_bytes = (inst.bm + inst.bn) * inst.bk * 2
+    return N <= 0 or inst.bm * -(-N // inst.bn) * 8 <= stage_bytes
 
 
 class GemmBiasLayerNormDescriptor(InstanceDescriptor):
@@ -82,18 +101,29 @@ class GemmBiasLayerNormDescriptor(InstanceDescriptor):
                     continue
                 if strategy == "row" and N and (N > inst.bn or inst.bn >= 2 * N):
                     continue  # whole row must fit one tile without wasting half of it
+                if strategy == "coresident" and not coresident_fits(inst, N):
+                    continue
                 raw = raw_from_inst(inst)
                 raw["strategy"] = strategy
                 out.append(raw)
         return out
 
     def format_config(self, raw):
-        return super().format_config(raw) + {"row": "_ROW", "gemm_ln": "_GL"}.get(raw.get("strategy"), "_2P")
+        return super().format_config(raw) + SUFFIX[raw.get("strategy", "two_pass")]
 
     def extra_seconds(self, raw, hw, M=0, N=0, K=0, **kw):
-        """Two-pass and GEMM-then-LN run a second launch that reads and writes Y."""
-        if raw.get("strategy") == "row":
+        """Two-pass and GEMM-then-LN run a second launch that reads and writes Y; the
+        co-resident strategy waits once per launch for its row blocks' statistics
+        (about one device-memory round trip each way, ~4 us), one launch per chunk of
+        row blocks one workgroup per CU holds."""
+        strategy = raw.get("strategy")
+        if strategy == "row":
             return 0.0
+        if strategy == "coresident":
+            tiles_n = -(-N // raw["block_N"]) if N else 1
+            tiles_m = -(-M // raw["block_M"]) if M else 1
+            per_launch = max(1, hw.num_sm // max(1, tiles_n))
+            return 4e-6 * -(-tiles_m // per_launch)
         op = self.make_op_spec(raw, M=M, N=N, K=K)
         return extra_pass_seconds(op, hw, 2.0 * M * N * op.mainloop.output_element_bytes)
 
@@ -122,7 +152,7 @@ def _overlap(a: torch.Tensor, b: torch.Tensor) -> bool:
 class CompiledGemmLayerNorm:
     def __init__(self, M, N, K, config, eps=1e-5):
         self.M, self.N, self.K, self.config, self.eps = M, N, K, config, eps
-        self.family = STRATEGY_FAMILY[config.get("strategy", "two_pass")]
+        self.family = STRATEGY_CALL[config.get("strategy", "two_pass")]
         self.inst = DESCRIPTOR.instance_index(config)
         self._ws: Optional[torch.Tensor] = None
 
@@ -131,7 +161,7 @@ class CompiledGemmLayerNorm:
         ``out``) is the add of the BERT attention-output / FFN-output blocks (end2end.py:76-79)."""
         need = runtime.ln_workspace_bytes(self.family, self.inst, self.M, self.N, self.K)
         if need and (self._ws is None or self._ws.device != A.device):
-            self._ws = runtime.alloc_workspace(need, A.device)
+            self._ws = runtime.alloc_workspace(need, A.device, zeroed=self.family == "gemm_ln_cr")
         if self.family == "gemm" and residual is not None and out is not None and _overlap(out, residual):
             # GEMM-then-LN writes Y before reading the residual: go through a fresh output
             y = runtime.gemm_bias_layernorm(self.family, self.inst, A, B, bias, gamma, beta, eps=self.eps,
@@ -151,4 +181,4 @@ def build_fused_kernel(M, N, K, gemm_config=None, block_M_ln=16, block_N_ln=128,
     return CompiledGemmLayerNorm(M, N, K, gemm_config, eps=eps)
 
 
-__all__ = ["DESCRIPTOR", "GemmBiasLayerNormDescriptor", "STRATEGY_FAMILY", "build_fused_kernel", "get_gemm_configs"]
+__all__ = ["DESCRIPTOR", "GemmBiasLayerNormDescriptor", "STRATEGY_CALL", "STRATEGY_FAMILY", "coresident_fits", "build_fused_kernel", "get_gemm_configs"]

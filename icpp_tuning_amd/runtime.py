@@ -12,7 +12,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import ACT, CONV_EPI, DTYPE, FAMILY, lib
+from ._lib import ACT, CONV_EPI, DTYPE, FAMILY, LN_STRATEGY, lib
 
 TORCH_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
 OUT_DTYPE = {"f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.bfloat16}
@@ -47,14 +47,20 @@ def workspace_bytes(family: str, inst: int, M: int, N: int, K: int, split_k: int
 
 
 def ln_workspace_bytes(family: str, inst: int, M: int, N: int, K: int) -> int:
-    """Workspace of a GEMM+bias+LayerNorm call (icpp_gemm_bias_layernorm_workspace_bytes)."""
-    return lib().ln_workspace_bytes(FAMILY[family], inst, M, N, K)
+    """Workspace of a GEMM+bias+LayerNorm call (icpp_gemm_bias_layernorm_workspace_bytes);
+    family is an instance family name or "gemm_ln_cr" (co-resident, an f16 GEMM instance)."""
+    return lib().ln_workspace_bytes(LN_STRATEGY[family], inst, M, N, K)
 
 
-def alloc_workspace(nbytes: int, device) -> Optional[torch.Tensor]:
+def alloc_workspace(nbytes: int, device, zeroed: bool = False) -> Optional[torch.Tensor]:
+    """A workspace of at least nbytes (16-byte aligned); zeroed for the co-resident
+    LayerNorm, whose counter block must start at zero (each call leaves it zero)."""
     if nbytes <= 0:
         return None
-    return torch.empty((nbytes + 15) // 16 * 4, dtype=torch.float32, device=device)
+    shape = ((nbytes + 15) // 16 * 4,)
+    if zeroed:
+        return torch.zeros(shape, dtype=torch.float32, device=device)
+    return torch.empty(shape, dtype=torch.float32, device=device)
 
 
 def gemm(inst: int, dtype: str, a: torch.Tensor, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
@@ -99,15 +105,15 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
     py = _check(out, "out", h, (M, N), device=a.device)
     need = ln_workspace_bytes(family, inst, M, N, K)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = alloc_workspace(need, a.device)
+        workspace = alloc_workspace(need, a.device, zeroed=family == "gemm_ln_cr")
     pws = workspace.data_ptr() if (need and workspace is not None) else None
     wsb = workspace.numel() * workspace.element_size() if (need and workspace is not None) else 0
     if residual is None:
-        lib().call("icpp_gemm_bias_layernorm", FAMILY[family], inst, pa, pb, pbias, pg, pbe, py,
+        lib().call("icpp_gemm_bias_layernorm", LN_STRATEGY[family], inst, pa, pb, pbias, pg, pbe, py,
                    M, N, K, float(eps), pws, wsb, _stream())
     else:
         pr = _check(residual, "residual", h, (M, N), device=a.device)
-        lib().call("icpp_gemm_bias_residual_layernorm", FAMILY[family], inst, pa, pb, pbias, pr, pg, pbe, py,
+        lib().call("icpp_gemm_bias_residual_layernorm", LN_STRATEGY[family], inst, pa, pb, pbias, pr, pg, pbe, py,
                    M, N, K, float(eps), pws, wsb, _stream())
     return out
 

@@ -39,6 +39,13 @@ enum icpp_family {
   ICPP_NUM_FAMILIES = 4
 };
 
+/*
+ * Strategy code for the LayerNorm entry points, beside the families above (it is
+ * not an instance family): `inst` is an f16 ICPP_FAMILY_GEMM instance, run with
+ * the co-resident row-block epilogue (see icpp_gemm_bias_layernorm).
+ */
+enum { ICPP_LN_CORESIDENT = 16 };
+
 enum icpp_dtype { ICPP_F16 = 0, ICPP_BF16 = 1, ICPP_FP8_E4M3 = 2, ICPP_F32 = 3 /* row ops only */ };
 enum icpp_act { ICPP_ACT_NONE = 0, ICPP_ACT_RELU = 1, ICPP_ACT_GELU_TANH = 2, ICPP_ACT_SILU = 3,
                 ICPP_ACT_GELU_ERF = 4 /* 0.5 x (1 + erf(x / sqrt 2)), torch's default F.gelu */ };
@@ -98,6 +105,16 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
  * two-launch strategies here keep X in Y as f16 values centred on the mean of
  * their (row, wave column block), with that mean in fp32 in the workspace, so a
  * row offset far above the row's spread loses no precision.
+ * ICPP_LN_CORESIDENT (inst: an f16 ICPP_FAMILY_GEMM instance whose tile has
+ * block_m >= 64, block_n >= 128 and 2+ stages) is one launch per row chunk with
+ * no X in memory: every launch holds only as many row blocks as the device keeps
+ * resident at once, and the workgroups of a row block exchange their (mean, M2)
+ * through the workspace and normalise their tiles from registers.  Its workspace
+ * (icpp_gemm_bias_layernorm_workspace_bytes) ends in a counter block that must be
+ * zero before the first call on it; every call leaves it zero.  Calls that share a
+ * workspace, or that run at the same time on different streams, must not overlap.
+ * ICPP_E_SHAPE when one row block cannot be resident at once (N too wide for the
+ * tile) or its statistics do not fit one LDS stage array.
  */
 int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
                              const void* gamma, const void* beta, void* Y,
@@ -123,10 +140,14 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
 
 /*
  * Workspace bytes icpp_gemm_bias_layernorm / icpp_gemm_bias_residual_layernorm need
- * for `family` (ICPP_FAMILY_GEMM_LN_ROW, _LN_STATS or ICPP_FAMILY_GEMM) and instance
- * (0 when none).  It holds what the reference keeps in its fp32 X intermediate
- * (gemm_bias_layernorm.py:175-186 allocates it per call): per-(row, column block)
- * statistics, M * ceil(N / wave tile columns) * 4 or * 8 bytes.
+ * for `family` (ICPP_FAMILY_GEMM_LN_ROW, _LN_STATS, ICPP_FAMILY_GEMM or
+ * ICPP_LN_CORESIDENT) and instance (0 when none).  It holds what the reference keeps
+ * in its fp32 X intermediate (gemm_bias_layernorm.py:175-186 allocates it per call):
+ * per-(row, column block) statistics, M * ceil(N / wave tile columns) * 4 or * 8
+ * bytes; for ICPP_LN_CORESIDENT M * ceil(N / block_n) * 8 bytes (16-byte aligned),
+ * then 16 bytes whose first int is set to 1 if a row block's wait ran out (its
+ * workgroups were not resident together: the call's output is then invalid), then
+ * the counters, 8 bytes per block_m rows.
  */
 size_t icpp_gemm_bias_layernorm_workspace_bytes(int family, int inst, int M, int N, int K);
 

@@ -91,8 +91,37 @@ def test_validation_errors_before_launch(L):
     assert fr(gem, ibf, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
     assert fr(gem, i16, 16, 16, None, 4096 + 64, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -4
     assert "overlap" in L.last_error()
+    # co-resident LayerNorm: f16 GEMM tiles that carry its kernel only (no bf16, no
+    # 32-row tiles), checked before any device query
+    cr = _lib.LN_CORESIDENT
+    i32 = next(i for i, t in enumerate(gems) if t.dtype == "f16" and t.bm < 64)
+    assert fr(cr, ibf, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
+    assert fr(cr, i32, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
+    assert "co-resident" in L.last_error()
+    assert fr(cr, i16, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, -1.0, None, 0, None) == -4  # eps
     c = L._dll.icpp_conv2d_nhwc
     assert c(0, 16, 16, 16, 1, 8, 8, 3, 64, 3, 3, 1, 1, 1, 1, None, 0, None) == -2  # C % 8
+
+
+def test_coresident_workspace_layout(L):
+    """ICPP_LN_CORESIDENT workspace: M x ceil(N / block_n) (mean, M2) fp32 pairs, 16-byte
+    aligned, then a 16-byte error block, then two int counters per block_m rows; none
+    for tiles without the co-resident kernel."""
+    from icpp_tuning_amd.kernels import gemm_bias_layernorm as ln_mod
+
+    gems = family_instances("gemm")
+    n_cr = 0
+    for i, t in enumerate(gems):
+        for M, N in ((333, 776), (8192, 4096), (1, 8)):
+            got = L.ln_workspace_bytes(_lib.LN_CORESIDENT, i, M, N, 512)
+            if not ln_mod.coresident_fits(t, 0):
+                assert got == 0, t.name
+                continue
+            pairs = M * -(-N // t.bn) * 8
+            assert got == -(-pairs // 16) * 16 + 16 + -(-M // t.bm) * 8, (t.name, M, N)
+        n_cr += ln_mod.coresident_fits(t, 0)
+    assert n_cr >= 20
+    assert L.ln_workspace_bytes(_lib.LN_CORESIDENT, len(gems), 64, 64, 64) == 0
 
 
 def test_fused_conv_validation_errors_before_launch(L):

@@ -57,7 +57,9 @@ def test_rescore_repicks_the_formula_against_stored_times():
 
 def test_layernorm_second_pass_is_priced():
     """Two-pass and GEMM-then-LN launch a pass that reads and writes Y once more;
-    the one-launch row strategy does not."""
+    the one-launch row strategy does not; the co-resident one pays ~4 us of statistics
+    exchange per launch, one launch per chunk of row blocks the CUs hold (256 // tiles_n
+    row blocks per launch)."""
     from icpp_tuning_amd.autotuner import rank_all
     from icpp_tuning_amd.autotuner.cost_model import CDNA4_CONSTANTS as C
 
@@ -69,10 +71,14 @@ def test_layernorm_second_pass_is_priced():
         strategy = e["raw_config"]["strategy"]
         seen.add(strategy)
         want = 0.0 if strategy == "row" else 2 * M * N * 2 / (8000e9 * C.hbm_efficiency) + C.launch_overhead_s
+        if strategy == "coresident":
+            raw = e["raw_config"]
+            per_launch = 256 // -(-N // raw["block_N"])
+            want = 4e-6 * -(-(-(-M // raw["block_M"])) // per_launch)
         assert e["detail"]["extra_s"] == pytest.approx(want), e["formatted"]
         if strategy == "gemm_ln":      # a plain GEMM + bias launch: no statistics epilogue
             assert [p.name for p in desc.make_op_spec(e["raw_config"], M=M, N=N, K=K).epilogue] == ["bias_add"]
-    assert seen == {"row", "two_pass", "gemm_ln"}
+    assert seen == {"row", "two_pass", "gemm_ln", "coresident"}
 
 
 def test_report_topk_is_the_best_measured_of_the_ranking():

@@ -34,7 +34,7 @@ def _close(y, ref, rtol, atol, what):
     assert not bad.any(), f"{what}: {int(bad.sum())} / {y.numel()} outside tol, max err {err.max().item():.4g}"
 
 
-@pytest.mark.parametrize("strategy", ["row", "two_pass", "gemm_ln"])
+@pytest.mark.parametrize("strategy", ["row", "two_pass", "gemm_ln", "coresident"])
 def test_residual_layernorm_every_instance(gpu, strategy):
     M, N, K = 200, 768, 512
     d = I.gemm_inputs(M, N, K, torch.float16, 60, b_std=1 / math.sqrt(K), bias=True)
@@ -46,6 +46,8 @@ def test_residual_layernorm_every_instance(gpu, strategy):
     fam = ln_mod.STRATEGY_FAMILY[strategy]
     for inst in family_instances(fam):
         if K % inst.bk or (strategy == "row" and N > inst.bn) or inst.dtype != "f16":
+            continue
+        if strategy == "coresident" and not ln_mod.coresident_fits(inst, N):
             continue
         raw = raw_from_inst(inst)
         raw["strategy"] = strategy

@@ -66,6 +66,20 @@ def test_graph_gemm_ln_two_pass(gpu):
     _replay_check(lambda: k(*args, out=Y), [Y], "gemm+ln two-pass")
 
 
+def test_graph_gemm_ln_coresident(gpu):
+    """The co-resident LayerNorm's counters return to zero at the end of every launch,
+    so graph replays (two chunks per replay here) give the eager result each time."""
+    M, N, K = 4000, 4096, 256
+    d = I.config3(M, N, K)
+    inst = next(i for i in family_instances("gemm") if i.name == "gemm_f16_256x256x64_w2x4_m16_s2_pp")
+    raw = raw_from_inst(inst)
+    raw["strategy"] = "coresident"
+    k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+    args = [d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")]
+    Y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    _replay_check(lambda: k(*args, out=Y), [Y], "gemm+ln co-resident")
+
+
 def test_graph_conv_splitk(gpu):
     Nb, H, W, C, F = 2, 14, 14, 256, 256
     d = I.config4(Nb, H, W, C, F)

@@ -164,7 +164,7 @@ C3_OFFSETS = I.C3_OFFSETS
 
 
 @pytest.mark.parametrize("kind", C3_OFFSETS)
-@pytest.mark.parametrize("strategy", ["row", "two_pass", "gemm_ln"])
+@pytest.mark.parametrize("strategy", ["row", "two_pass", "gemm_ln", "coresident"])
 def test_every_ln_instance_offset_rows(gpu, strategy, kind):
     """Every instance of each LayerNorm strategy on rows far from zero (ragged M and N;
     N = the row tile's width for whole-row instances)."""
@@ -175,6 +175,8 @@ def test_every_ln_instance_offset_rows(gpu, strategy, kind):
         if inst.dtype != "f16" or K % inst.bk:
             continue
         N = inst.bn if strategy == "row" else 776
+        if strategy == "coresident" and not ln_mod.coresident_fits(inst, N):
+            continue
         if N not in refs:
             d = I.config3_offset(M, N, K, kind)
             refs[N] = (d, O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"]))
@@ -201,7 +203,7 @@ def test_config3_offset_rows_every_strategy(gpu, N, kind):
     dev = {t: d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")}
     configs, seen = [], set()
     ranked = rank_all(ln_mod.DESCRIPTOR, M=M, N=N, K=K)
-    for strategy in ("row", "two_pass", "gemm_ln"):
+    for strategy in ("row", "two_pass", "gemm_ln", "coresident"):
         top = next((e["raw_config"] for e in ranked if e["raw_config"].get("strategy") == strategy), None)
         if top is not None:
             configs.append(top)
@@ -218,7 +220,61 @@ def test_config3_offset_rows_every_strategy(gpu, N, kind):
         torch.cuda.synchronize()
         _close(y, ref, 2e-2, 2e-2, f"config3 offset {kind} N={N} {name}")
         ran += 1
-    assert ran >= (3 if N <= 1024 else 2)
+    assert ran >= (4 if N <= 1024 else 3)
+
+
+def _cr_counters(k, M, N, bn, bm):
+    """(error word, counter block) of a co-resident LayerNorm workspace: M * ceil(N / bn)
+    (mean, M2) pairs, 16-byte aligned, then 16 bytes whose first int is the error flag,
+    then 2 ints per block_m rows."""
+    ws = k._ws.view(torch.int32).cpu()
+    stats = M * -(-N // bn) * 2
+    err = (stats + 3) // 4 * 4
+    return int(ws[err]), ws[err + 4: err + 4 + 2 * -(-M // bm)]
+
+
+def test_coresident_every_instance(gpu):
+    """Every f16 GEMM tile with the co-resident LayerNorm kernel on ragged M and N, called
+    twice in a row (the counters must return to zero and the error flag stay clear)."""
+    M, N, K = 333, 776, 512
+    d = I.config3(M, N, K)
+    ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+    dev = [d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")]
+    ran = 0
+    for inst in family_instances("gemm"):
+        if K % inst.bk or not ln_mod.coresident_fits(inst, N):
+            continue
+        raw = raw_from_inst(inst)
+        raw["strategy"] = "coresident"
+        print(f"[parity] co-resident {inst.name} M={M} N={N} K={K}", flush=True)
+        k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+        for call in range(2):
+            y = k(*dev)
+            torch.cuda.synchronize()
+            _close(y, ref, 2e-2, 2e-2, f"{inst.name} co-resident call {call}")
+            err, ctr = _cr_counters(k, M, N, inst.bn, inst.bm)
+            assert err == 0 and not ctr.any(), f"{inst.name}: error flag {err}, counters {ctr.tolist()}"
+        ran += 1
+    assert ran >= 10
+
+
+@pytest.mark.parametrize("M", [8192, 5000])
+def test_coresident_chunks(gpu, M):
+    """Row blocks beyond what the device holds at once go out in several launches (the
+    256 x 256 tile at N = 4096: 16 row blocks per launch), the last one ragged at M = 5000."""
+    N, K = 4096, 256
+    d = I.config3(M, N, K)
+    ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+    inst = next(i for i in family_instances("gemm") if i.name == "gemm_f16_256x256x64_w2x4_m16_s2_pp")
+    raw = raw_from_inst(inst)
+    raw["strategy"] = "coresident"
+    print(f"[parity] co-resident chunks {inst.name} M={M} N={N} K={K}", flush=True)
+    k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+    y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
+    torch.cuda.synchronize()
+    _close(y, ref, 2e-2, 2e-2, f"co-resident chunks M={M}")
+    err, ctr = _cr_counters(k, M, N, inst.bn, inst.bm)
+    assert err == 0 and not ctr.any()
 
 
 def test_every_conv_instance(gpu):
