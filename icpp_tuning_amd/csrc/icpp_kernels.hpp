@@ -722,16 +722,18 @@ gemm_kernel(KArgs p) {
   // (g, ow) reads halo pixel (g - g0 + kh) * W + ow + kw - 1, or Z when its input
   // column or row lies outside the image.  Without zero border columns, consecutive
   // output pixels read consecutive halo pixels also across image rows, so the
-  // chunk swizzle c ^ ((q >> 1) & 7) keeps its pattern where an MFMA row band
+  // chunk swizzle c ^ (swz(q) & 7) keeps its pattern where an MFMA row band
   // straddles an image row (with the border columns of an earlier layout, the
   // pixel index jumped by 3 there: 24.6% and 39.2% LDS bank conflicts on the
-  // 256 x 64 (32x32 MFMA) and 224 x 64 (16x16) tiles at 56 x 56 x 64, 17.0% and
-  // 37.8% with this layout).  The K tiles are the 9 taps.
+  // 256 x 64 (32x32 MFMA) and 224 x 64 (16x16) tiles at 56 x 56 x 64).  swz(q) is
+  // q >> 1 for 32x32 fragment reads and q for 16x16 ones, the best of 20 swizzles
+  // measured with the conflict counters on both tiles: 17.0% and 18.0% (q >> 1 on
+  // the 16x16 tile: 37.8%).  The K tiles are the 9 taps.
   constexpr int HL = HALO ? (HALO_CAP / 16 + G::THREADS - 1) / G::THREADS : 1;  // halo loads per thread
   int h_q[HALO ? G::TM : 1];       // halo pixel of this lane's row of MFMA tile tm at tap (0, 0)
   int h_vmask[HALO ? G::TM : 1];   // bit kh * 3 + kw: tap (kh, kw) reads inside the image
   int h_z = 0;                     // the zero pixel Z
-  auto halo_swz = [&](int q) ICPP_INLINE { return (q >> 1) & 7; };
+  auto halo_swz = [&](int q) ICPP_INLINE { return (MF == 16 ? q : q >> 1) & 7; };
   // the halo rows of item it: first output row g0 and the number of halo rows
   auto halo_rows = [&](const Item& it, int& g0, int& rows) ICPP_INLINE {
     g0 = it.row0 / p.cW;

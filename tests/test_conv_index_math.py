@@ -81,7 +81,7 @@ def _halo_tile(Nb, H, W, BM, MF, row0, wave_rows):
     g0 = row0 // W
     rows = (min(row0 + BM, M) - 1) // W - g0 + 3
     zpix = rows * W
-    swz = lambda q: (q >> 1) & 7
+    swz = (lambda q: q & 7) if MF == 16 else (lambda q: (q >> 1) & 7)
     lds = {}
     for s in range((zpix + 1) * 8):                 # issue_halo
         q = s >> 3
