@@ -81,12 +81,14 @@ LnCrLayout ln_cr_layout(const icpp_tile_t& t, int M, int N) {
 
 // Workgroups of an instance's co-resident LayerNorm kernel the current device holds at
 // once: CUs x workgroups per CU (the occupancy query, capped by the LDS a CU has).
-int ln_cr_capacity(const Instance* in) {
+int ln_cr_capacity(const Instance* in, int* cus_out = nullptr) {
   int dev = 0, cus = 0;
+  if (cus_out) *cus_out = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   int per_cu = in->resident_ln_cr ? in->resident_ln_cr() : 0;
   per_cu = std::min(per_cu, (160 * 1024) / std::max(1, in->tile.lds_bytes));
+  if (cus_out) *cus_out = std::max(0, cus);
   return std::max(0, cus) * std::max(0, per_cu);
 }
 
@@ -294,7 +296,8 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
     if ((size_t)t.block_m * a.tiles_n * 2 * sizeof(float) > (size_t)gi->ln_cr_stage_bytes)
       return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: N=%d is too wide for %s: a row block's statistics exceed one LDS stage",
                   N, t.name);
-    const int cap = ln_cr_capacity(gi);
+    int cus = 0;
+    const int cap = ln_cr_capacity(gi, &cus);
     if (cap < a.tiles_n)
       return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: %s: the %d tiles of a row block cannot be resident at once (%d)",
                   t.name, a.tiles_n, cap);
@@ -305,11 +308,37 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
     char* w = (char*)workspace;
     int* ctr = (int*)(w + l.ctr_off);
     a.ln_err = (int*)(w + l.err_off);
-    // even chunks of at most cap / tiles_n row blocks
     const int max_rows = cap / a.tiles_n;
+    hipStream_t s = (hipStream_t)stream;
+    if (a.tiles_m > max_rows && cus % 8 == 0) {
+      // More row blocks than the device holds at once: one launch in rounds of R row
+      // blocks, when the round splits into 8 equal per-XCD blocks of (R / xa) x
+      // (tiles_n / xb) tiles that fit each XCD's share of the CUs (the fewest A + B
+      // panels per XCD); otherwise even chunks, one launch each.  (Every XCD has the
+      // same share of the CUs only when their count divides by 8.)
+      int best_a = 0, best_cost = 1 << 30;
+      const int per_xcd = cap / 8;
+      for (int xa = 1; xa <= 8; xa *= 2) {
+        const int xb = 8 / xa;
+        if (max_rows % xa || a.tiles_n % xb) continue;
+        if ((max_rows / xa) * (a.tiles_n / xb) > per_xcd) continue;
+        const int cost = max_rows / xa + a.tiles_n / xb;
+        if (cost < best_cost) best_cost = cost, best_a = xa;
+      }
+      if (best_a) {
+        KArgs b = a;
+        b.cr_rows = max_rows;
+        b.cr_xa = best_a;
+        b.cr_xb = 8 / best_a;
+        b.ws = (float*)w;
+        b.ln_ctr = ctr;
+        const int rounds = ceil_div(a.tiles_m, max_rows);
+        return check_launch(gi->launch_ln_cr(b, dim3(rounds * max_rows * a.tiles_n), s), t.name);
+      }
+    }
+    // even chunks of at most cap / tiles_n row blocks
     const int chunks = ceil_div(a.tiles_m, max_rows);
     const int chunk_tm = ceil_div(a.tiles_m, chunks);
-    hipStream_t s = (hipStream_t)stream;
     for (int tm0 = 0; tm0 < a.tiles_m; tm0 += chunk_tm) {
       const int r0 = tm0 * t.block_m;
       KArgs b = a;

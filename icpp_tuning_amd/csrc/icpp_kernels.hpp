@@ -116,6 +116,10 @@ struct KArgs {
   const void* residual;    // LayerNorm epilogues: [M, ldc] (output type) added before the statistics, or null
   int* ln_ctr;             // EPI_LN_CR: [tiles_m][2] arrival / departure counters (zero between calls)
   int* ln_err;             // EPI_LN_CR: set to 1 when a row block's wait ran out
+  // EPI_LN_CR in rounds (0: one workgroup per tile in the usual order): each round of
+  // cr_rows row blocks is split into 8 per-XCD blocks of cr_rows / cr_xa row blocks x
+  // tiles_n / cr_xb tile columns
+  int cr_rows, cr_xa, cr_xb;
 };
 
 template <int DT> struct DTraits;
@@ -613,7 +617,24 @@ gemm_kernel(KArgs p) {
     const int gm = min(p.tiles_m - first_m, GROUP);
     return Item{(first_m + (t % group_size) % gm) * BM, ((t % group_size) / gm) * BN, kz};
   };
-  const Item first = item_of(slot);
+  // EPI_LN_CR with more row blocks than the device holds at once runs in rounds, each a
+  // set of whole row blocks that fits the device.  Workgroup b runs on XCD b % 8, and
+  // each XCD starts its workgroups in order, so XCD x's k-th workgroup belongs to round
+  // k / (its share of a round): a round's row blocks are all resident before any
+  // workgroup of the next one takes a CU, and none of their waits depends on a later
+  // round.  Within a round, XCD x takes block (x / cr_xb, x % cr_xb) of the round's
+  // row blocks x tile columns, so its L2 holds as few A and B panels as the usual order.
+  auto cr_item = [&]() ICPP_INLINE {
+    const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int rx = p.cr_rows / p.cr_xa, cx = p.tiles_n / p.cr_xb;
+    const int r = k / (rx * cx), pp = k % (rx * cx);
+    const int rb = r * p.cr_rows + (x / p.cr_xb) * rx + pp % rx;
+    const int tc = (x % p.cr_xb) * cx + pp / rx;
+    return Item{rb * BM, tc * BN, 0};
+  };
+  const Item first = (EPI == EPI_LN_CR && p.cr_rows > 0) ? cr_item() : item_of(slot);
+  // a last round with fewer row blocks than a full one: its spare workgroups have no tile
+  if (EPI == EPI_LN_CR && first.row0 >= p.M) return;
   const int nk = min(p.k_split, p.K - first.kz * p.k_split) / BK;  // K tiles of the item (>= 1)
 
   // ---- global -> LDS: buffer_load_dwordx4 ... lds (16 B per lane, range-checked:

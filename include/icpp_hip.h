@@ -106,10 +106,13 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
  * their (row, wave column block), with that mean in fp32 in the workspace, so a
  * row offset far above the row's spread loses no precision.
  * ICPP_LN_CORESIDENT (inst: an f16 ICPP_FAMILY_GEMM instance whose tile has
- * block_m >= 64, block_n >= 128 and 2+ stages) is one launch per row chunk with
- * no X in memory: every launch holds only as many row blocks as the device keeps
- * resident at once, and the workgroups of a row block exchange their (mean, M2)
- * through the workspace and normalise their tiles from registers.  Its workspace
+ * block_m >= 64, block_n >= 128 and 2+ stages) keeps X in registers: the
+ * workgroups of a row block exchange their (mean, M2) through the workspace and
+ * normalise their tiles from registers.  Row blocks beyond what the device keeps
+ * resident at once run in rounds of one launch (each XCD starts its workgroups in
+ * order, and a round's row blocks are all resident before the next round's take
+ * a CU), or in even chunks, one launch each, when a round does not split over the
+ * 8 XCDs.  Its workspace
  * (icpp_gemm_bias_layernorm_workspace_bytes) ends in a counter block that must be
  * zero before the first call on it; every call leaves it zero.  Calls that share a
  * workspace, or that run at the same time on different streams, must not overlap.

@@ -258,21 +258,25 @@ def test_coresident_every_instance(gpu):
     assert ran >= 10
 
 
-@pytest.mark.parametrize("M", [8192, 5000])
-def test_coresident_chunks(gpu, M):
-    """Row blocks beyond what the device holds at once go out in several launches (the
-    256 x 256 tile at N = 4096: 16 row blocks per launch), the last one ragged at M = 5000."""
-    N, K = 4096, 256
+@pytest.mark.parametrize("M,N,tile", [(8192, 4096, "gemm_f16_256x256x64_w2x4_m16_s2_pp"),
+                                       (5000, 4096, "gemm_f16_256x256x64_w2x4_m16_s2_pp"),
+                                       (11000, 768, "gemm_f16_256x128x64_w2x4_m16_s2")])
+def test_coresident_rounds_and_chunks(gpu, M, N, tile):
+    """Row blocks beyond what the device holds at once: the 256 x 256 tile at N = 4096 runs
+    one launch in rounds of 16 row blocks (8 x 4 tiles per XCD), the last round ragged at
+    M = 5000 (its spare workgroups exit); at N = 768 the 256 x 128 tile's 6 tile columns do
+    not split over 8 XCDs, so its 43 row blocks go out in even chunks, one launch each."""
+    K = 128
     d = I.config3(M, N, K)
     ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
-    inst = next(i for i in family_instances("gemm") if i.name == "gemm_f16_256x256x64_w2x4_m16_s2_pp")
+    inst = next(i for i in family_instances("gemm") if i.name == tile)
     raw = raw_from_inst(inst)
     raw["strategy"] = "coresident"
-    print(f"[parity] co-resident chunks {inst.name} M={M} N={N} K={K}", flush=True)
+    print(f"[parity] co-resident rounds / chunks {inst.name} M={M} N={N} K={K}", flush=True)
     k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
     y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
     torch.cuda.synchronize()
-    _close(y, ref, 2e-2, 2e-2, f"co-resident chunks M={M}")
+    _close(y, ref, 2e-2, 2e-2, f"co-resident rounds / chunks {tile} M={M}")
     err, ctr = _cr_counters(k, M, N, inst.bn, inst.bm)
     assert err == 0 and not ctr.any()
 
