@@ -5,7 +5,10 @@
 #include <stdio.h>
 #include <string.h>
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "icpp_registry.hpp"
@@ -81,15 +84,30 @@ LnCrLayout ln_cr_layout(const icpp_tile_t& t, int M, int N) {
 
 // Workgroups of an instance's co-resident LayerNorm kernel the current device holds at
 // once: CUs x workgroups per CU (the occupancy query, capped by the LDS a CU has).
+// (The CU count and the occupancy are queried once per device and instance.)
 int ln_cr_capacity(const Instance* in, int* cus_out = nullptr) {
-  int dev = 0, cus = 0;
+  static std::mutex mu;
+  static std::map<std::pair<int, const Instance*>, std::pair<int, int>> cache;  // -> (cus, per CU)
+  int dev = 0;
   if (cus_out) *cus_out = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  int per_cu = in->resident_ln_cr ? in->resident_ln_cr() : 0;
-  per_cu = std::min(per_cu, (160 * 1024) / std::max(1, in->tile.lds_bytes));
-  if (cus_out) *cus_out = std::max(0, cus);
-  return std::max(0, cus) * std::max(0, per_cu);
+  std::pair<int, int> v;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dev, in});
+    if (it != cache.end()) {
+      v = it->second;
+    } else {
+      int cus = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+      int per_cu = in->resident_ln_cr ? in->resident_ln_cr() : 0;
+      per_cu = std::min(per_cu, (160 * 1024) / std::max(1, in->tile.lds_bytes));
+      v = {std::max(0, cus), std::max(0, per_cu)};
+      cache[{dev, in}] = v;
+    }
+  }
+  if (cus_out) *cus_out = v.first;
+  return v.first * v.second;
 }
 
 hipError_t launch_splitk_reduce(int dt, const float* ws, void* C, const void* bias, int M, int N, int ldc,
