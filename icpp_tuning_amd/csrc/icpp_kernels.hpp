@@ -558,6 +558,20 @@ struct HaloLds<false, N> {
   static __device__ __forceinline__ char ICPP_LDS* ptr() { return nullptr; }
 };
 
+// Stage arrays 4..7 of the deeper rings, likewise present only in the kernels that use
+// them (each index its own object).
+template <bool ON, int N, int I>
+struct ExtraStage {
+  static __device__ __forceinline__ char ICPP_LDS* ptr() {
+    __shared__ __attribute__((aligned(16))) char stage[N];
+    return (char ICPP_LDS*)stage;
+  }
+};
+template <int N, int I>
+struct ExtraStage<false, N, I> {
+  static __device__ __forceinline__ char ICPP_LDS* ptr() { return nullptr; }
+};
+
 template <int DT, int BM, int BN, int BK, int WM, int WN, int MF, int STAGES, int EPI, int ALOAD>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_kernel(KArgs p) {
@@ -594,12 +608,14 @@ gemm_kernel(KArgs p) {
   char ICPP_LDS* const halo_lds = HaloLds<HALO, HALO_CAP>::ptr();
   static_assert(!HALO || (G::ESZ == 2 && BK == 64), "A_HALO: 16-bit data, one 64-channel chunk per pixel");
   static_assert(!HALO || SBYTES * STAGES + HALO_CAP <= 160 * 1024, "A_HALO: LDS overflow");
+  static_assert(STAGES >= 1 && STAGES <= 8, "1 to 8 pipeline stages");
   auto stage_base = [&](auto S) -> char ICPP_LDS* ICPP_INLINE {
     constexpr int s = decltype(S)::value;
     if constexpr (s == 0) return (char ICPP_LDS*)lds0;
     else if constexpr (s == 1) return (char ICPP_LDS*)lds1;
     else if constexpr (s == 2) return (char ICPP_LDS*)lds2;
-    else return (char ICPP_LDS*)lds3;
+    else if constexpr (s == 3) return (char ICPP_LDS*)lds3;
+    else return ExtraStage<(STAGES > s), SBYTES, s>::ptr();
   };
 
   const int tid = threadIdx.x;
