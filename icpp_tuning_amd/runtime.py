@@ -93,7 +93,10 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
                         eps: float = 1e-5, workspace: Optional[torch.Tensor] = None,
                         residual: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out = LayerNorm_N(a @ b + bias [+ residual]) * gamma + beta through icpp_gemm_bias_layernorm
-    (or icpp_gemm_bias_residual_layernorm with a residual [M, N] f16; it may be out itself)."""
+    (or icpp_gemm_bias_residual_layernorm with a residual [M, N] f16; it may be out itself).
+    family "gemm_ln_cr" (an f16 "gemm" instance) is the co-resident strategy: a workspace
+    passed in must have been zero-filled once (alloc_workspace(..., zeroed=True)); the
+    calls keep it zero, and calls sharing it must not overlap in time."""
     M, K = a.shape
     _, N = b.shape
     h = torch.float16
