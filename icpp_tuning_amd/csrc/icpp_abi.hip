@@ -332,7 +332,9 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
       // More row blocks than the device holds at once: one launch in rounds of R row
       // blocks, when the round splits into 8 equal per-XCD blocks of (R / xa) x
       // (tiles_n / xb) tiles that fit each XCD's share of the CUs (the fewest A + B
-      // panels per XCD); otherwise even chunks, one launch each.  (Every XCD has the
+      // panels per XCD, and among those the most row splits: a row block then spans
+      // the fewest XCDs and waits on fewer of them); otherwise even chunks, one launch
+      // each.  (Every XCD has the
       // same share of the CUs only when their count divides by 8.)
       int best_a = 0, best_cost = 1 << 30;
       const int per_xcd = cap / 8;
@@ -341,7 +343,7 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
         if (max_rows % xa || a.tiles_n % xb) continue;
         if ((max_rows / xa) * (a.tiles_n / xb) > per_xcd) continue;
         const int cost = max_rows / xa + a.tiles_n / xb;
-        if (cost < best_cost) best_cost = cost, best_a = xa;
+        if (cost <= best_cost) best_cost = cost, best_a = xa;
       }
       if (best_a) {
         KArgs b = a;

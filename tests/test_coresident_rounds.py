@@ -2,7 +2,7 @@
 
 Python mirrors of the launcher's round plan (`icpp_abi.hip`, ICPP_LN_CORESIDENT: the
 8-way split of a round's row blocks x tile columns with the fewest A + B panels per
-XCD) and of the kernel's workgroup -> tile map (`icpp_kernels.hpp`, `cr_item`), and a
+XCD, ties going to the most row splits) and of the kernel's workgroup -> tile map (`icpp_kernels.hpp`, `cr_item`), and a
 discrete-event model of the dispatch they rely on: workgroup b runs on XCD b % 8, each
 XCD starts its workgroups in order when one of its CUs is free, and a workgroup holds
 its CU until every tile of its row block has arrived.  The model checks that every row
@@ -26,7 +26,7 @@ def round_plan(tiles_m, tiles_n, cap):
         xb = 8 // xa
         if R % xa == 0 and tiles_n % xb == 0 and (R // xa) * (tiles_n // xb) <= cap // 8:
             cost = R // xa + tiles_n // xb
-            if cost < best_cost:
+            if cost <= best_cost:
                 best, best_cost = (R, xa, xb), cost
         xa *= 2
     return best
@@ -97,11 +97,12 @@ def test_round_map_covers_every_tile_once(tiles_m, tiles_n, cap):
     assert len(seen) == tiles_m * tiles_n
 
 
-def test_c3_n4096_plan_is_eight_by_four_per_xcd():
+def test_c3_n4096_plan_is_four_by_eight_per_xcd():
     """256 x 256 tiles at M = 8192, N = 4096 on 256 CUs: 2 rounds of 16 row blocks, each XCD
-    holding 8 row blocks x 4 tile columns (the L2 footprint of the usual order)."""
+    holding 4 row blocks x 8 tile columns -- 12 A + B panels, the L2 footprint of the usual
+    order's 8 x 4, with each row block on 2 XCDs instead of 4."""
     R, xa, xb = round_plan(32, 16, 256)
-    assert (R, R // xa, 16 // xb) == (16, 8, 4)
+    assert (R, R // xa, 16 // xb) == (16, 4, 8)
 
 
 def test_plans_that_do_not_split_fall_back_to_chunks():
