@@ -97,3 +97,33 @@ def test_noalloc_rejects_partials_beyond_the_scratch(gpu):
                                       ctypes.c_float(d["scale_b"]), sk, torch.cuda.current_stream().cuda_stream)
     assert rc == -3, rc  # ICPP_E_WORKSPACE
     assert "static scratch" in lib().last_error()
+
+
+def test_noalloc_captured_in_a_graph(gpu):
+    """After a first eager call on the device (the one that resolves the scratch array's
+    address), a split-K icpp_gemm_noalloc call is captured in a HIP graph; every replay,
+    with eager work in between, matches icpp_gemm with a caller workspace bitwise."""
+    name, dtype, M, N, K, sk, act = "gemm_bf16_128x128x64_w2x2_m16_s2", "bf16", 200, 1032, 1024, 4, "gelu_tanh"
+    idx, _ = _inst(name)
+    d = I.gemm_inputs(M, N, K, runtime.TORCH_DTYPE[dtype], 93, b_std=1 / math.sqrt(K), bias=True, device="cuda")
+    ref = _with_workspace(idx, dtype, d["A"], d["B"], d["bias"], act, sk)
+    out = torch.empty((M, N), dtype=runtime.OUT_DTYPE[dtype], device="cuda")
+
+    def run():
+        lib().call("icpp_gemm_noalloc", idx, d["A"].data_ptr(), d["B"].data_ptr(), d["bias"].data_ptr(),
+                   out.data_ptr(), M, N, K, K, N, N, ACT[act], 1.0, 1.0, sk,
+                   torch.cuda.current_stream().cuda_stream)
+
+    run()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    torch.cuda.synchronize()
+    for r in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {r} differs"
