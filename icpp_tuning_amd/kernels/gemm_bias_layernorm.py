@@ -4,7 +4,7 @@ Mirrors kernel/tilelang/gemm/gemm_bias_layernorm.py: ``get_gemm_configs``
 (:19-40), ``build_fused_kernel`` (:167-188, ``fused(A, B, bias, gamma, beta) ->
 Y``) and ``DESCRIPTOR`` (:196-208).  The reference launches a GEMM+bias kernel
 that writes X in fp32 and then a separate two-pass row LayerNorm kernel that
-reads X twice and computes var = E[x^2] - mean^2 (:143).  Two strategies here,
+reads X twice and computes var = E[x^2] - mean^2 (:143).  Four strategies here,
 chosen per shape by the tuner:
 
   "row"       (gemm_ln_row)    one workgroup owns whole rows (N <= block_N):

@@ -99,8 +99,9 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
  * Replaces build_fused_kernel (gemm_bias_layernorm.py:167-188: GEMM+bias kernel
  * :61-88 followed by the row LayerNorm kernel :101-162).  `family` selects the
  * strategy: ICPP_FAMILY_GEMM_LN_ROW (whole row per workgroup, N <= block_n,
- * no workspace) or ICPP_FAMILY_GEMM_LN_STATS (GEMM writes X into Y plus
- * per-block (mean, M2) into the workspace, then a finalize pass normalises Y).
+ * no workspace), ICPP_FAMILY_GEMM_LN_STATS (GEMM writes X into Y plus
+ * per-block (mean, M2) into the workspace, then a finalize pass normalises Y),
+ * ICPP_FAMILY_GEMM (below) or ICPP_LN_CORESIDENT (below).
  * The reference keeps X in fp32 between its two kernels (:59, :66, :103); the
  * two-launch strategies here keep X in Y as f16 values centred on the mean of
  * their (row, wave column block), with that mean in fp32 in the workspace, so a
