@@ -170,6 +170,14 @@ class CompiledGemmLayerNorm:
         return runtime.gemm_bias_layernorm(self.family, self.inst, A, B, bias, gamma, beta, out=out,
                                            eps=self.eps, workspace=self._ws, residual=residual)
 
+    def wait_failed(self, clear: bool = False) -> bool:
+        """Co-resident strategy: whether a call since the flag was last cleared ran out of its
+        bounded wait (its output is then invalid; see runtime.coresident_wait_failed).  False
+        for the other strategies.  Synchronises."""
+        if self.family != "gemm_ln_cr" or self._ws is None:
+            return False
+        return runtime.coresident_wait_failed(self._ws, self.inst, self.M, self.N, clear=clear)
+
 
 def build_fused_kernel(M, N, K, gemm_config=None, block_M_ln=16, block_N_ln=128, thread_num_ln=128, eps=1e-5):
     """``fused(A, B, bias, gamma, beta) -> Y``.  The ``*_ln`` tile arguments of the

@@ -121,6 +121,30 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
     return out
 
 
+def coresident_layout(inst: int, M: int, N: int) -> tuple:
+    """(error word index, counter index, counter count) of a co-resident LayerNorm workspace
+    viewed as int32: M * ceil(N / block_n) (mean, M2) fp32 pairs, padded to 16 bytes, then
+    16 bytes whose first int is the error word, then two counters per block_m rows."""
+    from .instances import INSTANCES
+    t = sorted((i for i in INSTANCES if i.family == "gemm"), key=lambda i: i.name)[inst]
+    err = (M * -(-N // t.bn) * 2 + 3) // 4 * 4
+    return err, err + 4, 2 * -(-M // t.bm)
+
+
+def coresident_wait_failed(workspace: torch.Tensor, inst: int, M: int, N: int, clear: bool = False) -> bool:
+    """Whether a co-resident LayerNorm call on this workspace ran out of its bounded wait: a
+    row block's workgroups were not resident together (another kernel holding CUs, or two
+    calls on the workspace overlapping), and that call's output is invalid.  The word
+    stays set across calls until cleared (clear=True).  Reads device memory: synchronises
+    the current stream."""
+    err, _, _ = coresident_layout(inst, M, N)
+    words = workspace.view(torch.int32)
+    failed = bool(words[err].item())
+    if failed and clear:
+        words[err] = 0
+    return failed
+
+
 def conv2d_nhwc(inst: int, x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, stride: int = 1, pad: int = 1,
                 dilation: int = 1, split_k: int = 1, workspace: Optional[torch.Tensor] = None, *,
                 act: str = "none", bn: Optional[tuple] = None, eps: float = 1e-5, var_clamp: bool = False,

@@ -150,8 +150,9 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
  * per-(row, column block) statistics, M * ceil(N / wave tile columns) * 4 or * 8
  * bytes; for ICPP_LN_CORESIDENT M * ceil(N / block_n) * 8 bytes (16-byte aligned),
  * then 16 bytes whose first int is set to 1 if a row block's wait ran out (its
- * workgroups were not resident together: the call's output is then invalid), then
- * the counters, 8 bytes per block_m rows.
+ * workgroups were not resident together: the call's output is then invalid; the
+ * word stays set until the caller clears it), then the counters, 8 bytes per
+ * block_m rows.
  */
 size_t icpp_gemm_bias_layernorm_workspace_bytes(int family, int inst, int M, int N, int K);
 

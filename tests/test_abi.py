@@ -8,7 +8,7 @@ from pathlib import Path
 
 import pytest
 
-from icpp_tuning_amd import _lib
+from icpp_tuning_amd import _lib, runtime
 from icpp_tuning_amd.instances import INSTANCES
 from icpp_tuning_amd.kernels._base import family_instances
 
@@ -119,6 +119,9 @@ def test_coresident_workspace_layout(L):
                 continue
             pairs = M * -(-N // t.bn) * 8
             assert got == -(-pairs // 16) * 16 + 16 + -(-M // t.bm) * 8, (t.name, M, N)
+            # the runtime's int32 view of it (error word, counters) ends where the library's does
+            err, ctr, n = runtime.coresident_layout(i, M, N)
+            assert err * 4 == -(-pairs // 16) * 16 and ctr == err + 4 and (ctr + n) * 4 == got, (t.name, M, N)
         n_cr += ln_mod.coresident_fits(t, 0)
     assert n_cr >= 20
     assert L.ln_workspace_bytes(_lib.LN_CORESIDENT, len(gems), 64, 64, 64) == 0

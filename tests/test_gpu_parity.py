@@ -223,14 +223,11 @@ def test_config3_offset_rows_every_strategy(gpu, N, kind):
     assert ran >= (4 if N <= 1024 else 3)
 
 
-def _cr_counters(k, M, N, bn, bm):
-    """(error word, counter block) of a co-resident LayerNorm workspace: M * ceil(N / bn)
-    (mean, M2) pairs, 16-byte aligned, then 16 bytes whose first int is the error flag,
-    then 2 ints per block_m rows."""
-    ws = k._ws.view(torch.int32).cpu()
-    stats = M * -(-N // bn) * 2
-    err = (stats + 3) // 4 * 4
-    return int(ws[err]), ws[err + 4: err + 4 + 2 * -(-M // bm)]
+def _cr_counters(k, M, N):
+    """(wait-failed flag, counter block) of a co-resident LayerNorm kernel's workspace, read
+    through the runtime's layout of it."""
+    _, ctr, n = runtime.coresident_layout(k.inst, M, N)
+    return k.wait_failed(), k._ws.view(torch.int32).cpu()[ctr: ctr + n]
 
 
 def test_coresident_every_instance(gpu):
@@ -252,7 +249,7 @@ def test_coresident_every_instance(gpu):
             y = k(*dev)
             torch.cuda.synchronize()
             _close(y, ref, 2e-2, 2e-2, f"{inst.name} co-resident call {call}")
-            err, ctr = _cr_counters(k, M, N, inst.bn, inst.bm)
+            err, ctr = _cr_counters(k, M, N)
             assert err == 0 and not ctr.any(), f"{inst.name}: error flag {err}, counters {ctr.tolist()}"
         ran += 1
     assert ran >= 10
@@ -277,7 +274,7 @@ def test_coresident_rounds_and_chunks(gpu, M, N, tile):
     y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
     torch.cuda.synchronize()
     _close(y, ref, 2e-2, 2e-2, f"co-resident rounds / chunks {tile} M={M}")
-    err, ctr = _cr_counters(k, M, N, inst.bn, inst.bm)
+    err, ctr = _cr_counters(k, M, N)
     assert err == 0 and not ctr.any()
 
 
