@@ -489,8 +489,9 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
         return build_sampling_plan(op, hw, m_range=(16, 4096), nk=[(4096, 4096), (11008, 4096), (4096, 11008)],
                                    points_per_wave=2)
     if op == "gemm_bias_layernorm":   # C3 shapes, BERT-base's attention-output and FFN-output blocks, and the
-        # reference's evaluation shape (N = 2304, K = 768: gemm_three_ops_formula_summary.csv)
-        return build_sampling_plan(op, hw, m_range=(128, 8192),
+        # reference's evaluation shape (N = 2304, K = 768: gemm_three_ops_formula_summary.csv,
+        # M = 1 ... 126), from decode-sized M up
+        return build_sampling_plan(op, hw, m_range=(16, 8192),
                                    nk=[(768, 4096), (1024, 4096), (4096, 4096), (768, 768), (768, 3072), (2304, 768)],
                                    points_per_wave=2)
     if op == "gemm_bias_gelu_erf":     # BERT-base's FFN-in block (end2end.py:82-83)

@@ -80,7 +80,7 @@ Instance make_instance(int family, const char* name) {
     in.launch = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI, AL>;
     in.launch_gather = nullptr;
   }
-  if constexpr (DT == DT_F16 && EPI == EPI_STORE && (AL & 7) == A_DENSE && BM >= 64 && BN >= 128 && ST >= 2) {
+  if constexpr (DT == DT_F16 && EPI == EPI_STORE && (AL & 7) == A_DENSE && ST >= 2) {
     in.launch_ln_cr = &launch_instance<DT, BM, BN, BK, WM, WN, MF, ST, EPI_LN_CR, AL>;
     in.resident_ln_cr = &resident_per_cu<DT, BM, BN, BK, WM, WN, MF, ST, EPI_LN_CR, AL>;
     in.ln_cr_stage_bytes = G::STAGE_BYTES;

@@ -48,11 +48,11 @@ SUFFIX = {"row": "_ROW", "two_pass": "_2P", "gemm_ln": "_GL", "coresident": "_CR
 
 
 def coresident_fits(inst, N: int) -> bool:
-    """The f16 GEMM tiles built with the co-resident LayerNorm kernel (block_m >= 64,
-    block_n >= 128, 2+ stages), for row widths whose block_m x ceil(N / block_n)
-    (mean, M2) pairs fit one LDS stage array; the library also checks that one row
-    block's ceil(N / block_n) workgroups fit the device at once."""
-    if inst.family != "gemm" or inst.dtype != "f16" or inst.bm < 64 or inst.bn < 128 or inst.stages < 2:
+    """The f16 GEMM tiles built with the co-resident LayerNorm kernel (every f16 GEMM
+    tile with 2+ stages), for row widths whose block_m x ceil(N / block_n) (mean, M2)
+    pairs fit one LDS stage array; the library also checks that one row block's
+    ceil(N / block_n) workgroups fit the device at once."""
+    if inst.family != "gemm" or inst.dtype != "f16" or inst.stages < 2:
         return False
     stage_bytes = (inst.bm + inst.bn) * inst.bk * 2
     return N <= 0 or inst.bm * -(-N // inst.bn) * 8 <= stage_bytes

@@ -106,8 +106,8 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
  * two-launch strategies here keep X in Y as f16 values centred on the mean of
  * their (row, wave column block), with that mean in fp32 in the workspace, so a
  * row offset far above the row's spread loses no precision.
- * ICPP_LN_CORESIDENT (inst: an f16 ICPP_FAMILY_GEMM instance whose tile has
- * block_m >= 64, block_n >= 128 and 2+ stages) keeps X in registers: the
+ * ICPP_LN_CORESIDENT (inst: an f16 ICPP_FAMILY_GEMM instance whose tile has 2+
+ * stages) keeps X in registers: the
  * workgroups of a row block exchange their (mean, M2) through the workspace and
  * normalise their tiles from registers.  Row blocks beyond what the device keeps
  * resident at once run in rounds of one launch (each XCD starts its workgroups in

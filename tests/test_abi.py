@@ -91,13 +91,13 @@ def test_validation_errors_before_launch(L):
     assert fr(gem, ibf, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
     assert fr(gem, i16, 16, 16, None, 4096 + 64, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -4
     assert "overlap" in L.last_error()
-    # co-resident LayerNorm: f16 GEMM tiles that carry its kernel only (no bf16, no
-    # 32-row tiles), checked before any device query
+    # co-resident LayerNorm: f16 GEMM tiles only (every one carries its kernel; bf16 and
+    # fp8 tiles do not), checked before any device query
     cr = _lib.LN_CORESIDENT
-    i32 = next(i for i, t in enumerate(gems) if t.dtype == "f16" and t.bm < 64)
-    assert fr(cr, ibf, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
-    assert fr(cr, i32, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
-    assert "co-resident" in L.last_error()
+    i8 = next(i for i, t in enumerate(gems) if t.dtype == "fp8")
+    for bad in (ibf, i8):
+        assert fr(cr, bad, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, 1e-5, None, 0, None) == -1
+        assert "co-resident" in L.last_error()
     assert fr(cr, i16, 16, 16, None, None, 16, 16, 4096, 64, 64, 64, -1.0, None, 0, None) == -4  # eps
     c = L._dll.icpp_conv2d_nhwc
     assert c(0, 16, 16, 16, 1, 8, 8, 3, 64, 3, 3, 1, 1, 1, 1, None, 0, None) == -2  # C % 8
