@@ -490,10 +490,13 @@ def default_plan(op: str, hw: Optional[GPUSpec] = None) -> List[Dict[str, int]]:
                                    points_per_wave=2)
     if op == "gemm_bias_layernorm":   # C3 shapes, BERT-base's attention-output and FFN-output blocks, and the
         # reference's evaluation shape (N = 2304, K = 768: gemm_three_ops_formula_summary.csv,
-        # M = 1 ... 126), from decode-sized M up
-        return build_sampling_plan(op, hw, m_range=(16, 8192),
-                                   nk=[(768, 4096), (1024, 4096), (4096, 4096), (768, 768), (768, 3072), (2304, 768)],
-                                   points_per_wave=2)
+        # M = 1 ... 126), from decode-sized M up.  Below 128 rows every 16 rows: the one-launch
+        # strategy's time steps with the row-block count, which a power-of-two grid misses
+        nk = [(768, 4096), (1024, 4096), (4096, 4096), (768, 768), (768, 3072), (2304, 768)]
+        plan = build_sampling_plan(op, hw, m_range=(16, 8192), nk=nk, points_per_wave=2)
+        have = {(s["M"], s["N"], s["K"]) for s in plan}
+        plan += [dict(M=m, N=n, K=k) for n, k in nk for m in range(16, 128, 16) if (m, n, k) not in have]
+        return plan
     if op == "gemm_bias_gelu_erf":     # BERT-base's FFN-in block (end2end.py:82-83)
         return build_sampling_plan(op, hw, m_range=(128, 16384), nk=[(3072, 768), (4096, 1024)], points_per_wave=2)
     # GEMM + bias + activation: C2's 4096-class shapes and the reference's evaluation shape
