@@ -311,9 +311,14 @@ int icpp_gemm_bias_residual_layernorm(int family, int inst, const void* A, const
                               1.f, 1, &gi, &a))
       return rc;
     const icpp_tile_t& t = gi->tile;
-    if ((size_t)t.block_m * a.tiles_n * 2 * sizeof(float) > (size_t)gi->ln_cr_stage_bytes)
-      return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: N=%d is too wide for %s: a row block's statistics exceed one LDS stage",
-                  N, t.name);
+    {
+      // a row block's [block_m][tiles_n] (mean, M2) pairs go to two stage arrays, an even
+      // number of rows in the first (the kernel's split), the rest in the second
+      const size_t per = (size_t)gi->ln_cr_stage_bytes / ((size_t)a.tiles_n * 2 * sizeof(float));
+      if ((size_t)t.block_m > (per & ~(size_t)1) + per)
+        return fail(ICPP_E_SHAPE, "icpp_gemm_bias_layernorm: N=%d is too wide for %s: a row block's statistics exceed two LDS stages",
+                    N, t.name);
+    }
     int cus = 0;
     const int cap = ln_cr_capacity(gi, &cus);
     if (cap < a.tiles_n)

@@ -1492,7 +1492,6 @@ gemm_kernel(KArgs p) {
         constexpr int LN_CR_SPINS = 1 << 17;  // ~0.1-0.3 s of polling before giving up
         __syncthreads();  // every wave is done with the mainloop's LDS
         float ICPP_LDS* red = (float ICPP_LDS*)lds0;  // [WN][BM] per-wave row sums, then M2
-        float ICPP_LDS* rowst = (float ICPP_LDS*)lds1;  // [BM][2] merged (mean, rstd)
         const int tcnt = max(0, min(BN, p.N - col0));
         const float inv_t = tcnt > 0 ? 1.f / (float)tcnt : 0.f;
         float tmean[G::TM];
@@ -1570,38 +1569,49 @@ gemm_kernel(KArgs p) {
           }
         }
         __syncthreads();
-        // The row block's pairs are one contiguous [BM][tiles_n][2] block of ws: 16-byte
-        // device-scope loads spread over the workgroup bring it into LDS (the launcher
-        // checks that it fits one stage array), then one thread per row merges it.
+        // The row block's pairs are one contiguous [rows][tiles_n][2] block of ws: 16-byte
+        // device-scope loads spread over the workgroup bring it into LDS -- rows [0, r0) into
+        // the first stage array, the rest into the second (r0 even, so the split falls on a
+        // 16-byte boundary; the launcher checks that both parts fit) -- then one thread per
+        // row merges its row and leaves the merged (mean, rstd) in the row's first pair.
+        const int rows = max(0, min(BM, p.M - row0));
+        const int prow = 2 * p.tiles_n;                                   // floats per row
+        const int r0 = min(rows, (SBYTES / (4 * prow)) & ~1);
+        auto row_pairs = [&](int r) ICPP_INLINE {
+          return r < r0 ? (float ICPP_LDS*)lds0 + r * prow : (float ICPP_LDS*)lds1 + (r - r0) * prow;
+        };
         {
-          float ICPP_LDS* pairs = (float ICPP_LDS*)lds0;
-          const int rows = max(0, min(BM, p.M - row0));
-          const int nvec = rows * p.tiles_n / 2;  // tiles_n pairs of 8 bytes per row; BM and rows*tiles_n even
+          const int nvec = rows * p.tiles_n / 2;  // 16-byte vectors: two pairs each
+          const int nvec0 = r0 * p.tiles_n / 2;   // those of rows [0, r0), exactly (r0 even)
           const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.ws + (size_t)row0 * p.tiles_n * 2, (uint32_t)(nvec * 16));
-          for (int i = tid; i < nvec; i += G::THREADS)
-            *(i32x4 ICPP_LDS*)(pairs + 4 * i) = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(i * 16), 0, 16);
+          for (int i = tid; i < nvec; i += G::THREADS) {
+            char ICPP_LDS* dst = i < nvec0 ? (char ICPP_LDS*)lds0 + 16 * i : (char ICPP_LDS*)lds1 + 16 * (i - nvec0);
+            *(i32x4 ICPP_LDS*)dst = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(i * 16), 0, 16);
+          }
           if ((rows * p.tiles_n) & 1) {  // an odd last pair (odd tiles_n and an odd row count)
             if (tid == 0) {
               const int j = rows * p.tiles_n - 1;
-              pairs[2 * j] = __hip_atomic_load(p.ws + ((size_t)row0 * p.tiles_n + j) * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              pairs[2 * j + 1] = __hip_atomic_load(p.ws + ((size_t)row0 * p.tiles_n + j) * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              float ICPP_LDS* dst = row_pairs(rows - 1) + 2 * (p.tiles_n - 1);
+              dst[0] = __hip_atomic_load(p.ws + ((size_t)row0 * p.tiles_n + j) * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              dst[1] = __hip_atomic_load(p.ws + ((size_t)row0 * p.tiles_n + j) * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
           }
           __syncthreads();
           for (int r = tid; r < rows; r += G::THREADS) {
+            float ICPP_LDS* pr = row_pairs(r);
             float n_acc = 0.f, mu = 0.f, m2 = 0.f;
             for (int j = 0; j < p.tiles_n; ++j) {
               const float nb = (float)max(0, min(BN, p.N - j * BN));
-              const float mb = pairs[(r * p.tiles_n + j) * 2 + 0];
-              const float qb = pairs[(r * p.tiles_n + j) * 2 + 1];
+              const float mb = pr[2 * j + 0];
+              const float qb = pr[2 * j + 1];
               const float nt = n_acc + nb;
               const float d = mb - mu;
               mu += d * (nb / nt);
               m2 += qb + d * d * (n_acc * nb / nt);
               n_acc = nt;
             }
-            rowst[2 * r + 0] = mu;
-            rowst[2 * r + 1] = rsqrtf(m2 / (float)p.N + p.eps);
+            pr[0] = mu;  // this thread alone reads and writes row r
+            pr[1] = rsqrtf(m2 / (float)p.N + p.eps);
           }
           __syncthreads();
         }
@@ -1619,8 +1629,11 @@ gemm_kernel(KArgs p) {
 #pragma unroll
         for (int tm = 0; tm < G::TM; ++tm) {
           const int lr = wm * G::WTM + tm * MF + (lane % MF);
-          mean[tm] = rowst[2 * lr + 0];
-          rstd[tm] = rowst[2 * lr + 1];
+          // rows past M (never stored) take the last valid row's values: every read stays
+          // inside the pairs' region
+          const float ICPP_LDS* pr = row_pairs(min(lr, rows - 1));
+          mean[tm] = pr[0];
+          rstd[tm] = pr[1];
         }
         store_staged([&](int tm, int tn, int g) ICPP_INLINE {
           f32x4 v;

@@ -50,12 +50,15 @@ SUFFIX = {"row": "_ROW", "two_pass": "_2P", "gemm_ln": "_GL", "coresident": "_CR
 def coresident_fits(inst, N: int) -> bool:
     """The f16 GEMM tiles built with the co-resident LayerNorm kernel (every f16 GEMM
     tile with 2+ stages), for row widths whose block_m x ceil(N / block_n) (mean, M2)
-    pairs fit one LDS stage array; the library also checks that one row block's
-    ceil(N / block_n) workgroups fit the device at once."""
+    pairs fit two LDS stage arrays (an even number of rows in the first, the rest in
+    the second, as the kernel splits them); the library also checks that one row
+    block's ceil(N / block_n) workgroups fit the device at once."""
     if inst.family != "gemm" or inst.dtype != "f16" or inst.stages < 2:
         return False
-    stage_bytes = (inst.bm + inst.bn) * inst.bk * 2
-    return N <= 0 or inst.bm * -(-N // inst.bn) * 8 <= stage_bytes
+    if N <= 0:
+        return True
+    per = (inst.bm + inst.bn) * inst.bk * 2 // (-(-N // inst.bn) * 8)
+    return inst.bm <= (per & ~1) + per
 
 
 class GemmBiasLayerNormDescriptor(InstanceDescriptor):

@@ -118,7 +118,7 @@ int icpp_gemm(int inst, const void* A, const void* B, const void* bias, void* C,
  * zero before the first call on it; every call leaves it zero.  Calls that share a
  * workspace, or that run at the same time on different streams, must not overlap.
  * ICPP_E_SHAPE when one row block cannot be resident at once (N too wide for the
- * tile) or its statistics do not fit one LDS stage array.
+ * tile) or its statistics do not fit two LDS stage arrays.
  */
 int icpp_gemm_bias_layernorm(int family, int inst, const void* A, const void* B, const void* bias,
                              const void* gamma, const void* beta, void* Y,

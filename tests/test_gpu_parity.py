@@ -255,6 +255,34 @@ def test_coresident_every_instance(gpu):
     assert ran >= 10
 
 
+def test_coresident_statistics_across_two_stages(gpu):
+    """Tiles whose row block's (mean, M2) pairs outgrow one LDS stage array at N = 2312
+    (37 tile columns of 64, 19 of 128): the kernel puts an even number of rows in the
+    first array and the rest in the second.  The last row block has an odd row count
+    and the tile-column count is odd, so the odd last pair lands in the second array."""
+    N, K = 2312, 256
+    ran = 0
+    for inst in family_instances("gemm"):
+        tiles_n = -(-N // inst.bn)
+        stage = (inst.bm + inst.bn) * inst.bk * 2
+        if K % inst.bk or not ln_mod.coresident_fits(inst, N) or inst.bm * tiles_n * 8 <= stage:
+            continue
+        M = 2 * inst.bm - 5
+        d = I.config3(M, N, K)
+        ref = O.gemm_bias_layernorm_ref(d["A"], d["B"], d["bias"], d["gamma"], d["beta"])
+        raw = raw_from_inst(inst)
+        raw["strategy"] = "coresident"
+        print(f"[parity] co-resident two-stage statistics {inst.name} M={M} N={N} K={K}", flush=True)
+        k = ln_mod.build_fused_kernel(M, N, K, gemm_config=raw)
+        y = k(*(d[t].cuda() for t in ("A", "B", "bias", "gamma", "beta")))
+        torch.cuda.synchronize()
+        _close(y, ref, 2e-2, 2e-2, f"{inst.name} two-stage statistics")
+        err, ctr = _cr_counters(k, M, N)
+        assert not err and not ctr.any(), f"{inst.name}: wait failed {err}, counters {ctr.tolist()}"
+        ran += 1
+    assert ran >= 3
+
+
 @pytest.mark.parametrize("M,N,tile", [(8192, 4096, "gemm_f16_256x256x64_w2x4_m16_s2_pp"),
                                        (5000, 4096, "gemm_f16_256x256x64_w2x4_m16_s2_pp"),
                                        (11000, 768, "gemm_f16_256x128x64_w2x4_m16_s2")])
