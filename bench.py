@@ -441,6 +441,7 @@ def vs_libraries():
     import torch
     import torch.nn.functional as F
 
+    from icpp_tuning_amd import runtime
     from icpp_tuning_amd.autotuner.interface import benchmark_ms, input_bytes, tune
     from icpp_tuning_amd.kernels import conv2d as CV
     from icpp_tuning_amd.kernels import fp8_gemm_bias_act as F8
@@ -504,7 +505,62 @@ def vs_libraries():
                             "sa": torch.tensor(float(d["scale_a"]), device="cuda"),
                             "sb": torch.tensor(float(d["scale_b"]), device="cuda"),
                             "bias16": d["bias"].to(torch.bfloat16)})
+    # decode rows over pre-packed weights (icpp_fp8_gemm_packed, one launch): the weights are
+    # packed once outside the timed region, as torch's side transposes B once for _scaled_mm
+    for (M, N, K) in ((16, 4096, 4096), (16, 11008, 4096), (16, 4096, 11008)):
+        sets = [F8.DESCRIPTOR.make_inputs(M=M, N=N, K=K)]
+        copies = max(1, min(16, -(-(600 << 20) // max(1, input_bytes(sets[0])))))
+        sets += [F8.DESCRIPTOR.make_inputs(M=M, N=N, K=K) for _ in range(copies - 1)]
+        packed = [runtime.fp8_pack_b(d["B"]) for d in sets]
+        outs = [torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in sets]
+        runs = [(lambda d=d, p=p, o=o: runtime.fp8_gemm_packed(d["A"], p, N, bias=d["bias"], out=o, act="silu",
+                                                              scale_a=d["scale_a"], scale_b=d["scale_b"]))
+                for d, p, o in zip(sets, packed, outs)]
+        reps = max(20, 2 * copies)
+        benchmark_ms(runs, warmup=copies, reps=reps)
+        ours = benchmark_ms(runs, warmup=copies, reps=reps)
+        tp = [{"A": d["A"], "Bt": d["B"].t().contiguous(), "sa": torch.tensor(float(d["scale_a"]), device="cuda"),
+               "sb": torch.tensor(float(d["scale_b"]), device="cuda"), "bias16": d["bias"].to(torch.bfloat16)}
+              for d in sets]
+        t = benchmark_ms([(lambda v=v: F.silu(torch._scaled_mm(v["A"], v["Bt"].t(), scale_a=v["sa"], scale_b=v["sb"],
+                                                               bias=v["bias16"], out_dtype=torch.bfloat16)))
+                          for v in tp], warmup=copies, reps=reps)
+        rows.append({"op": "fp8_gemm_bias_silu (packed B)", "shape": dict(M=M, N=N, K=K),
+                     "config": "icpp_fp8_gemm_packed", "us": round(ours * 1e3, 2),
+                     "tflops": round(2.0 * M * N * K / ours / 1e9, 1), "torch": "_scaled_mm + silu",
+                     "input_copies": copies, "torch_us": round(t * 1e3, 2), "speedup": round(t / ours, 3)})
+        print(f"[vs] fp8 packed {M}x{N}x{K}: {rows[-1]['us']} us vs _scaled_mm + silu {rows[-1]['torch_us']} us",
+              file=sys.stderr, flush=True)
+        del sets, packed, outs, runs, tp
+        torch.cuda.empty_cache()
     return rows
+
+
+def fp8_decode(M: int, N: int, K: int, steps: int, warmup: int):
+    """fp8 GEMM + bias + SiLU at M <= 16 over weights packed once (icpp_fp8_pack_b, outside
+    the timed region), `steps` launches captured in a graph and replayed round-robin over
+    input copies larger than the MALL (median of 3 replays); device time per launch, and the
+    bytes it must read (A, packed B, bias) and write."""
+    import torch
+
+    from icpp_tuning_amd import inputs as I
+    from icpp_tuning_amd import runtime
+
+    copies = max(2, min(32, -(-CACHE_BYTES // (K * N + M * K))))
+    sets = []
+    for _ in range(copies):
+        d = I.config5(M, N, K)
+        sets.append((d["A"].cuda(), runtime.fp8_pack_b(d["B"].cuda()), d["bias"].cuda(), d["scale_a"], d["scale_b"]))
+    outs = [torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in sets]
+    fns = [(lambda s=s, o=o: runtime.fp8_gemm_packed(s[0], s[1], N, bias=s[2], out=o, act="silu", scale_a=s[3],
+                                                    scale_b=s[4])) for s, o in zip(sets, outs)]
+    from icpp_tuning_amd.autotuner.interface import benchmark_ms
+
+    # graph replay: an eager launch from Python costs more host time than the kernel runs
+    us = benchmark_ms(fns, warmup=max(warmup, copies), reps=steps) * 1e3
+    nbytes = M * K + K * N + 4 * N + 2 * M * N
+    return {"M": M, "N": N, "K": K, "steps": steps, "input_copies": copies, "us_per_launch": round(us, 2),
+            "bytes": nbytes, "gbps": round(nbytes / us / 1e3, 1), "hbm_frac": round(nbytes / us / 1e3 / HBM_GBPS, 3)}
 
 
 def reference_eval():
@@ -750,6 +806,9 @@ def main():
     ap.add_argument("--reference-eval", action="store_true",
                     help="print the reference's own evaluation sweep (M = 1..126, N = 2304, K = 768, three ops) "
                          "with the no-measurement select against torch, and exit")
+    ap.add_argument("--fp8-decode", default="",
+                    help="M,N,K: time fp8 GEMM + bias + SiLU over pre-packed weights (icpp_fp8_gemm_packed) for "
+                         "--steps launches after --warmup over rotated input copies (for profiler runs), and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
@@ -760,6 +819,10 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
+    if args.fp8_decode:
+        print(json.dumps({"fp8_decode": fp8_decode(*(int(v) for v in args.fp8_decode.split(",")), args.steps,
+                                                   args.warmup)}), flush=True)
+        return 0
     if args.calibrate_copy:
         src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "icpp_softmax_scaled_masked",
     "icpp_gemm_bias_residual_layernorm", "icpp_qkv_split_heads", "icpp_merge_heads", "icpp_attention_fwd",
     "icpp_clock_probe", "icpp_gemm_noalloc", "icpp_gemm_bias_layernorm_workspace_bytes",
+    "icpp_fp8_pack_b", "icpp_fp8_gemm_packed",
 )
 CONV_EPI = {"bn": 1, "residual": 2, "var_clamp": 4}
 
@@ -85,6 +86,8 @@ _SIGNATURES = {
     "icpp_merge_heads": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "icpp_clock_probe": (_i, [_vp, ctypes.c_double, _vp]),
     "icpp_gemm_noalloc": (_i, [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _f, _i, _vp]),
+    "icpp_fp8_pack_b": (_i, [_vp, _vp, _i, _i, _vp]),
+    "icpp_fp8_gemm_packed": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _vp]),
 }
 
 

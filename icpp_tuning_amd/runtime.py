@@ -121,6 +121,37 @@ def gemm_bias_layernorm(family: str, inst: int, a: torch.Tensor, b: torch.Tensor
     return out
 
 
+def fp8_pack_b(b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """B [K, N] fp8 e4m3 (row-major) rearranged for fp8_gemm_packed through icpp_fp8_pack_b:
+    every 16-column block one contiguous run over K, each 128-deep K step 2 KiB in the
+    16x16x128 MFMA operand layout.  Returns (or fills) a uint8 tensor of K * N bytes.
+    Needs K % 128 == 0 and N % 16 == 0; run once per weight matrix."""
+    K, N = b.shape
+    pb = _check(b, "b", torch.float8_e4m3fn)
+    if out is None:
+        out = torch.empty(K * N, dtype=torch.uint8, device=b.device)
+    po = _check(out, "out", torch.uint8, (K * N,), device=b.device)
+    lib().call("icpp_fp8_pack_b", pb, po, K, N, _stream())
+    return out
+
+
+def fp8_gemm_packed(a: torch.Tensor, bp: torch.Tensor, N: int, bias: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None, act: str = "silu", scale_a: float = 1.0,
+                    scale_b: float = 1.0) -> torch.Tensor:
+    """out[M, N] (bf16) = act(scale_a*scale_b * a[M, K] @ B + bias[N]) for M <= 16, B given
+    packed by fp8_pack_b: one launch through icpp_fp8_gemm_packed."""
+    M, K = a.shape
+    pa = _check(a, "a", torch.float8_e4m3fn)
+    pb = _check(bp, "bp", torch.uint8, (K * N,), device=a.device)
+    pbias = _check(bias, "bias", torch.float32, (N,), device=a.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    pc = _check(out, "out", torch.bfloat16, (M, N), device=a.device)
+    lib().call("icpp_fp8_gemm_packed", pa, pb, pbias, pc, M, N, K, ACT[act], float(scale_a), float(scale_b),
+               _stream())
+    return out
+
+
 def coresident_layout(inst: int, M: int, N: int) -> tuple:
     """(error word index, counter index, counter count) of a co-resident LayerNorm workspace
     viewed as int32: M * ceil(N / block_n) (mean, M2) fp32 pairs, padded to 16 bytes, then

@@ -292,6 +292,27 @@ int icpp_gemm_noalloc(int inst, const void* A, const void* B, const void* bias, 
                       float scale_a, float scale_b, int split_k, void* stream);
 
 /*
+ * fp8 decode over pre-packed weights: no counterpart in the reference (which has
+ * no fp8 kernel).  For callers that keep B fixed across calls (weights in serving)
+ * and run M <= 16 rows at a time, where icpp_gemm needs split-K and a second launch.
+ *
+ * icpp_fp8_pack_b: Bp = B [K, N] (fp8 e4m3, row-major, N contiguous) rearranged
+ * so that each 16-column block is one contiguous run over K: for block nb and
+ * K step s (128 rows), 2 KiB at byte ((nb * K / 128 + s) * 64 + l) * 32, whose
+ * 32 bytes for lane l are B[128 s + 32 (l / 16) + t][16 nb + l % 16], t = 0..31
+ * (the 16x16x128 fp8 MFMA operand layout).  Bp holds K * N bytes, 16-byte aligned.
+ * Needs K % 128 == 0 and N % 16 == 0.  Run once per weight matrix.
+ *
+ * icpp_fp8_gemm_packed: C[M,N] = act(scale_a*scale_b * A[M,K] @ B[K,N] + bias[N])
+ * with B given packed; A fp8 row-major (lda = K), bias f32 or null, C bf16
+ * (ldc = N): the types and epilogue of icpp_gemm's fp8 instances.  1 <= M <= 16,
+ * K % 128 == 0, N % 16 == 0, 16-byte aligned pointers.  One launch, no workspace.
+ */
+int icpp_fp8_pack_b(const void* B, void* Bp, int K, int N, void* stream);
+int icpp_fp8_gemm_packed(const void* A, const void* Bp, const void* bias, void* C, int M, int N, int K, int act,
+                         float scale_a, float scale_b, void* stream);
+
+/*
  * Measurement aid, no counterpart in the reference (whose harness reads clocks
  * from the NVIDIA profiler, motivation/exp_2/profile.py:39-53): one wave reads the
  * shader-clock counter and the 100 MHz real-time counter, sleeps until `seconds`

@@ -200,3 +200,26 @@ def test_rowops_validation_errors_before_launch(L):
     assert bwd(*args, 16, 1024, None) == -3                                            # too small
     assert bwd(f16, None, *args[2:], 16, 1 << 30, None) == -4                          # null dy
     assert "icpp_layernorm_bwd" in L.last_error()
+
+
+def test_fp8_packed_decode_rejections_before_launch(L):
+    """icpp_fp8_pack_b / icpp_fp8_gemm_packed check every argument before any device work
+    (the pointers here are never dereferenced)."""
+    pk = L._dll.icpp_fp8_pack_b
+    assert pk(None, 32, 256, 64, None) == -4
+    assert pk(16, 32, 200, 64, None) == -2          # K % 128
+    assert pk(16, 32, 256, 40, None) == -2          # N % 16
+    assert pk(16, 33, 256, 64, None) == -4          # Bp misaligned
+    g = L._dll.icpp_fp8_gemm_packed
+    ok = dict(A=16, Bp=32, bias=None, C=48, M=4, N=64, K=256, act=3)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return g(a["A"], a["Bp"], a["bias"], a["C"], a["M"], a["N"], a["K"], a["act"], 1.0, 1.0, None)
+
+    assert call(M=0) == -2 and call(M=17) == -2
+    assert call(K=200) == -2 and call(N=40) == -2 and call(K=0) == -2
+    assert call(A=None) == -4 and call(C=None) == -4
+    assert call(act=9) == -4
+    assert call(A=24) == -4 and call(bias=8) == -4
+    assert "aligned" in L.last_error()
