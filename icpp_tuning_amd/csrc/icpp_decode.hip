@@ -1,6 +1,6 @@
-// fp8 e4m3 GEMM + bias + activation for decode-sized M (1..16) over pre-packed weights.
+// fp8 e4m3 GEMM + bias + activation for decode-sized M (1..32) over pre-packed weights.
 //
-// The split-K kernels read B [K, N] (N contiguous) in tiles: at M <= 16 a launch
+// The split-K kernels read B [K, N] (N contiguous) in tiles: at M <= 32 a launch
 // needs K split across workgroups to keep enough CUs streaming B, and the split
 // costs a second launch that sums the fp32 partials.  With the weights packed once
 // (static weights in serving) so that every 16-column block is one contiguous run
@@ -18,6 +18,8 @@
 // The MFMA takes the B block as its first operand (rows = output columns n) and
 // A as its second (columns = output rows m): result lane l holds m = l % 16 and
 // n = 16 nb + 4 (l / 16) + 0..3, four consecutive outputs of one row per lane.
+// M = 17..32 runs two row tiles per wave (rows 16 j + l % 16), both against the
+// same B fragment.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,11 +39,13 @@ using namespace icpp;
 constexpr int kDecodeWaves = 4;   // waves per workgroup, splitting the K steps
 constexpr int kDecodeUnroll = 8;  // K steps per wave whose loads are in flight together
 
-template <int ACT>
+// MT row tiles of 16 (M <= 16 MT): each K step's B fragment meets MT A fragments.
+template <int ACT, int MT>
 __global__ void __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves_per_eu(1, 2)))
 fp8_decode_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ bias,
                   __bf16* __restrict__ C, int M, int N, int K, float alpha) {
   typedef Mfma<DT_FP8, 16> Op;
+  constexpr int U = MT == 1 ? kDecodeUnroll : kDecodeUnroll / 2;  // steps per group: fragments in registers
   const int nb = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int S = K >> 7;
@@ -50,43 +54,54 @@ fp8_decode_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bp,
   const __amdgpu_buffer_rsrc_t br = make_rsrc(Bp + (size_t)nb * S * 2048, (uint32_t)(S * 2048));
   const uint32_t a_lane = (uint32_t)((lane & 15) * K + (lane >> 4) * 32);
   const uint32_t b_lane = (uint32_t)(lane * 32);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  // Groups of kDecodeUnroll steps, every load of a group issued before its MFMAs.  Steps
-  // past the end (the last group of a wave) read from an offset past both descriptors'
-  // ranges, so their fragments are zeros and add nothing.
-  for (int s = wave; s < S; s += kDecodeUnroll * kDecodeWaves) {
-    Op::Frag af[kDecodeUnroll], bf[kDecodeUnroll];
+  f32x4 acc[MT];
 #pragma unroll
-    for (int u = 0; u < kDecodeUnroll; ++u) {
+  for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Groups of U steps, every load of a group issued before its MFMAs.  Steps past the
+  // end (the last group of a wave) read from an offset past both descriptors' ranges,
+  // so their fragments are zeros and add nothing.
+  for (int s = wave; s < S; s += U * kDecodeWaves) {
+    Op::Frag af[U][MT], bf[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
       const int su = s + u * kDecodeWaves;
       const uint32_t bo = su < S ? b_lane + (uint32_t)su * 2048 : ICPP_OOB_OFFSET;
-      const uint32_t ao = su < S ? a_lane + (uint32_t)su * 128 : ICPP_OOB_OFFSET;
       const i32x4 b0 = buf_load16(br, bo), b1 = buf_load16(br, bo + 16);
-      const i32x4 a0 = buf_load16(ar, ao), a1 = buf_load16(ar, ao + 16);
       bf[u] = Op::Frag{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-      af[u] = Op::Frag{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const uint32_t ao = su < S ? a_lane + (uint32_t)(16 * j * K) + (uint32_t)su * 128 : ICPP_OOB_OFFSET;
+        const i32x4 a0 = buf_load16(ar, ao), a1 = buf_load16(ar, ao + 16);
+        af[u][j] = Op::Frag{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      }
     }
     // keep the group's loads ahead of its MFMAs (the scheduler would otherwise trickle
     // them in between, one K step in flight at a time)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < kDecodeUnroll; ++u) acc = Op::run(bf[u], af[u], acc);
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[j] = Op::run(bf[u], af[u][j], acc[j]);
   }
   // the waves' partial sums meet in LDS, added in wave order
-  __shared__ f32x4 part[kDecodeWaves][64];
-  part[wave][lane] = acc;
+  __shared__ f32x4 part[kDecodeWaves][MT][64];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) part[wave][j][lane] = acc[j];
   __syncthreads();
   if (wave != 0) return;
-  f32x4 v = part[0][lane];
-#pragma unroll
-  for (int w = 1; w < kDecodeWaves; ++w) v += part[w][lane];
-  const int m = lane & 15;
   const int n = nb * 16 + 4 * (lane >> 4);
-  if (m >= M) return;
   const f32x4 bv = bias ? *reinterpret_cast<const f32x4*>(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = act_fn<ACT>(v[e] * alpha + bv[e]);
-  Vec4Store<__bf16>::st(C + (size_t)m * N + n, v);
+  for (int j = 0; j < MT; ++j) {
+    f32x4 v = part[0][j][lane];
+#pragma unroll
+    for (int w = 1; w < kDecodeWaves; ++w) v += part[w][j][lane];
+    const int m = 16 * j + (lane & 15);
+    if (m >= M) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = act_fn<ACT>(v[e] * alpha + bv[e]);
+    Vec4Store<__bf16>::st(C + (size_t)m * N + n, v);
+  }
 }
 
 // One thread per 16 bytes of the packed layout: a strided gather from B [K, N].
@@ -134,10 +149,10 @@ int icpp_fp8_pack_b(const void* B, void* Bp, int K, int N, void* stream) {
 int icpp_fp8_gemm_packed(const void* A, const void* Bp, const void* bias, void* C, int M, int N, int K, int act,
                          float scale_a, float scale_b, void* stream) {
   if (!A || !Bp || !C) return icpp::set_last_error(ICPP_E_ARG, "icpp_fp8_gemm_packed: null tensor");
-  if (M < 1 || M > 16) return icpp::set_last_error(ICPP_E_SHAPE, "icpp_fp8_gemm_packed: M must be 1..16");
+  if (M < 1 || M > 32) return icpp::set_last_error(ICPP_E_SHAPE, "icpp_fp8_gemm_packed: M must be 1..32");
   if (K <= 0 || N <= 0 || K % 128 || N % 16)
     return icpp::set_last_error(ICPP_E_SHAPE, "icpp_fp8_gemm_packed: need K > 0, K % 128 == 0, N > 0 and N % 16 == 0");
-  if ((size_t)M * K >= ((size_t)1 << 31) || (size_t)K * 16 >= ((size_t)1 << 31))
+  if ((size_t)M * K >= ((size_t)1 << 31) || (size_t)K * 32 >= ((size_t)1 << 31))
     return icpp::set_last_error(ICPP_E_SHAPE, "icpp_fp8_gemm_packed: K too large");
   if (act < ICPP_ACT_NONE || act > ICPP_ACT_GELU_ERF)
     return icpp::set_last_error(ICPP_E_ARG, "icpp_fp8_gemm_packed: unknown activation");
@@ -150,13 +165,18 @@ int icpp_fp8_gemm_packed(const void* A, const void* Bp, const void* bias, void* 
   const uint8_t* b = (const uint8_t*)Bp;
   const float* bi = (const float*)bias;
   __bf16* c = (__bf16*)C;
-  switch (act) {
-    case ICPP_ACT_RELU: hipLaunchKernelGGL(fp8_decode_kernel<ACT_RELU>, grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
-    case ICPP_ACT_GELU_TANH: hipLaunchKernelGGL(fp8_decode_kernel<ACT_GELU_TANH>, grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
-    case ICPP_ACT_SILU: hipLaunchKernelGGL(fp8_decode_kernel<ACT_SILU>, grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
-    case ICPP_ACT_GELU_ERF: hipLaunchKernelGGL(fp8_decode_kernel<ACT_GELU_ERF>, grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
-    default: hipLaunchKernelGGL(fp8_decode_kernel<ACT_NONE>, grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
-  }
+  auto launch = [&](auto MT) {
+    constexpr int mt = decltype(MT)::value;
+    switch (act) {
+      case ICPP_ACT_RELU: hipLaunchKernelGGL((fp8_decode_kernel<ACT_RELU, mt>), grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
+      case ICPP_ACT_GELU_TANH: hipLaunchKernelGGL((fp8_decode_kernel<ACT_GELU_TANH, mt>), grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
+      case ICPP_ACT_SILU: hipLaunchKernelGGL((fp8_decode_kernel<ACT_SILU, mt>), grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
+      case ICPP_ACT_GELU_ERF: hipLaunchKernelGGL((fp8_decode_kernel<ACT_GELU_ERF, mt>), grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
+      default: hipLaunchKernelGGL((fp8_decode_kernel<ACT_NONE, mt>), grid, block, 0, s, a, b, bi, c, M, N, K, alpha); break;
+    }
+  };
+  if (M <= 16) launch(std::integral_constant<int, 1>{});
+  else launch(std::integral_constant<int, 2>{});
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ICPP_OK : icpp::set_last_error((int)e, "icpp_fp8_gemm_packed: launch failed");
 }

@@ -138,7 +138,7 @@ def fp8_pack_b(b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Ten
 def fp8_gemm_packed(a: torch.Tensor, bp: torch.Tensor, N: int, bias: Optional[torch.Tensor] = None,
                     out: Optional[torch.Tensor] = None, act: str = "silu", scale_a: float = 1.0,
                     scale_b: float = 1.0) -> torch.Tensor:
-    """out[M, N] (bf16) = act(scale_a*scale_b * a[M, K] @ B + bias[N]) for M <= 16, B given
+    """out[M, N] (bf16) = act(scale_a*scale_b * a[M, K] @ B + bias[N]) for M <= 32, B given
     packed by fp8_pack_b: one launch through icpp_fp8_gemm_packed."""
     M, K = a.shape
     pa = _check(a, "a", torch.float8_e4m3fn)

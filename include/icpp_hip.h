@@ -294,7 +294,7 @@ int icpp_gemm_noalloc(int inst, const void* A, const void* B, const void* bias, 
 /*
  * fp8 decode over pre-packed weights: no counterpart in the reference (which has
  * no fp8 kernel).  For callers that keep B fixed across calls (weights in serving)
- * and run M <= 16 rows at a time, where icpp_gemm needs split-K and a second launch.
+ * and run M <= 32 rows at a time, where icpp_gemm needs split-K and a second launch.
  *
  * icpp_fp8_pack_b: Bp = B [K, N] (fp8 e4m3, row-major, N contiguous) rearranged
  * so that each 16-column block is one contiguous run over K: for block nb and
@@ -305,7 +305,7 @@ int icpp_gemm_noalloc(int inst, const void* A, const void* B, const void* bias, 
  *
  * icpp_fp8_gemm_packed: C[M,N] = act(scale_a*scale_b * A[M,K] @ B[K,N] + bias[N])
  * with B given packed; A fp8 row-major (lda = K), bias f32 or null, C bf16
- * (ldc = N): the types and epilogue of icpp_gemm's fp8 instances.  1 <= M <= 16,
+ * (ldc = N): the types and epilogue of icpp_gemm's fp8 instances.  1 <= M <= 32,
  * K % 128 == 0, N % 16 == 0, 16-byte aligned pointers.  One launch, no workspace.
  */
 int icpp_fp8_pack_b(const void* B, void* Bp, int K, int N, void* stream);

@@ -217,7 +217,7 @@ def test_fp8_packed_decode_rejections_before_launch(L):
         a = dict(ok, **kw)
         return g(a["A"], a["Bp"], a["bias"], a["C"], a["M"], a["N"], a["K"], a["act"], 1.0, 1.0, None)
 
-    assert call(M=0) == -2 and call(M=17) == -2
+    assert call(M=0) == -2 and call(M=33) == -2
     assert call(K=200) == -2 and call(N=40) == -2 and call(K=0) == -2
     assert call(A=None) == -4 and call(C=None) == -4
     assert call(act=9) == -4

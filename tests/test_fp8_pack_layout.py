@@ -4,7 +4,8 @@
 kernel's bytes with it).  It is pinned here against the header's byte formula by
 brute force over every byte, and the decode kernel's lane arithmetic is replayed
 in numpy -- operand lane l of the 16x16x128 MFMA holding row / column l % 16 and K
-slice 32 (l / 16) .. +32, result lane l holding m = l % 16 and n = 4 (l / 16) + e --
+slice 32 (l / 16) .. +32, result lane l holding m = 16 j + l % 16 (row tile j) and
+n = 4 (l / 16) + e --
 to show that fragments read that way from the packed B and from row-major A
 reproduce A @ B exactly.  A planted mistake (the lane groups of B taken in the
 wrong order) must break that equality.  No GPU needed.
@@ -42,28 +43,30 @@ def decode_emulated(a: np.ndarray, bp: np.ndarray, M: int, N: int, K: int, b_gro
     K offset 128 s + 32 (l / 16); the MFMA sums, over the 4 lane groups and 32 positions,
     B-fragment(lane 16 g + n % 16) x A-fragment(lane 16 g + m)."""
     S = K // 128
+    MT = 1 if M <= 16 else 2           # row tiles of 16: rows 16 j + l % 16
     out = np.zeros((M, N), dtype=np.float64)
-    a_pad = np.zeros((16, K), dtype=np.float64)
+    a_pad = np.zeros((16 * MT, K), dtype=np.float64)
     a_pad[:M] = a
     for nb in range(N // 16):
         for s in range(S):
             step = bp[((nb * S + s) * 64) * 32:((nb * S + s) * 64 + 64) * 32].reshape(64, 32)
-            for res_lane in range(64):
-                m, n0 = res_lane % 16, 4 * (res_lane // 16)
-                if m >= M:
-                    continue
-                for e in range(4):
-                    n = n0 + e
-                    acc = 0.0
-                    for g in range(4):
-                        bfrag = step[16 * b_group_order[g] + n]
-                        afrag = a_pad[m, 128 * s + 32 * g: 128 * s + 32 * g + 32]
-                        acc += float(np.dot(bfrag, afrag))
-                    out[m, 16 * nb + n] += acc
+            for j in range(MT):
+                for res_lane in range(64):
+                    m, n0 = 16 * j + res_lane % 16, 4 * (res_lane // 16)
+                    if m >= M:
+                        continue
+                    for e in range(4):
+                        n = n0 + e
+                        acc = 0.0
+                        for g in range(4):
+                            bfrag = step[16 * b_group_order[g] + n]
+                            afrag = a_pad[m, 128 * s + 32 * g: 128 * s + 32 * g + 32]
+                            acc += float(np.dot(bfrag, afrag))
+                        out[m, 16 * nb + n] += acc
     return out
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 16, 128), (5, 32, 256), (16, 48, 384)])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 128), (5, 32, 256), (16, 48, 384), (17, 16, 128), (32, 32, 256)])
 def test_lane_arithmetic_reproduces_the_product(M, N, K):
     g = torch.Generator().manual_seed(M * 1000 + N + K)
     a = torch.randint(-3, 4, (M, K), generator=g).double().numpy()

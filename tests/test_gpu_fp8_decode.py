@@ -38,7 +38,8 @@ def test_pack_kernel_matches_the_layout(gpu, K, N):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (5, 4096, 4096), (16, 4096, 4096), (16, 11008, 4096),
-                                   (16, 4096, 11008), (3, 48, 384), (16, 16, 128)])
+                                   (16, 4096, 11008), (3, 48, 384), (16, 16, 128), (17, 4096, 4096),
+                                   (32, 4096, 11008), (23, 48, 384)])
 @pytest.mark.parametrize("act,with_bias", [("silu", True), ("none", False)])
 def test_decode_matches_oracle(gpu, M, N, K, act, with_bias):
     d = I.config5(M, N, K)
@@ -66,13 +67,14 @@ def test_decode_beside_the_split_k_path(gpu):
     _close(y_dec, y_split.float().cpu(), 1e-2, 1e-2, "decode vs split-K")
 
 
-def test_decode_rows_past_m_and_repeated_calls(gpu):
+@pytest.mark.parametrize("M", [7, 23])
+def test_decode_rows_past_m_and_repeated_calls(gpu, M):
     """Rows m >= M are never written (the output past them keeps its contents), and two
-    calls in a row on one output give identical results."""
-    M, N, K = 7, 256, 1024
+    calls in a row on one output give identical results (one and two row tiles)."""
+    N, K = 256, 1024
     d = I.config5(M, N, K)
     bp = runtime.fp8_pack_b(d["B"].cuda())
-    buf = torch.full((16, N), 3.0, dtype=torch.bfloat16, device="cuda")
+    buf = torch.full((32, N), 3.0, dtype=torch.bfloat16, device="cuda")
     out = buf[:M]
     a = d["A"].cuda()
     runtime.fp8_gemm_packed(a, bp, N, bias=d["bias"].cuda(), out=out, scale_a=d["scale_a"], scale_b=d["scale_b"])
