@@ -83,3 +83,26 @@ def test_decode_rows_past_m_and_repeated_calls(gpu, M):
     torch.cuda.synchronize()
     assert torch.equal(first, out)
     assert bool((buf[M:] == 3.0).all())
+
+
+def test_decode_in_a_graph(gpu):
+    """The decode call has no workspace and allocates nothing: captured in a HIP graph and
+    replayed three times, with eager work and a synchronize between replays, every replay
+    equals the eager result bit for bit."""
+    M, N, K = 16, 1024, 2048
+    d = I.config5(M, N, K)
+    a, bias = d["A"].cuda(), d["bias"].cuda()
+    bp = runtime.fp8_pack_b(d["B"].cuda())
+    eager = runtime.fp8_gemm_packed(a, bp, N, bias=bias, scale_a=d["scale_a"], scale_b=d["scale_b"])
+    out = torch.empty_like(eager)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        runtime.fp8_gemm_packed(a, bp, N, bias=bias, out=out, scale_a=d["scale_a"], scale_b=d["scale_b"])
+    for rep in range(3):
+        out.fill_(0.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+        _ = (a.float() * 2).sum().item()  # eager work between replays
