@@ -427,6 +427,25 @@ def bench_ops(quick: bool, only: str = "", fixed_configs: str = "", row_index: i
     for (M, N, K) in f8_shapes:
         record("fp8_gemm_bias_silu", F8.DESCRIPTOR, dict(M=M, N=N, K=K), 2.0 * M * N * K,
                M * K + K * N + 2 * M * N + 4 * N, "fp8")
+    # decode-sized fp8 over weights packed once (icpp_fp8_gemm_packed, one launch; the packing
+    # is outside the timed region, as weights are in serving)
+    from icpp_tuning_amd import inputs as I
+
+    def _decode(M, N, K):
+        def make(i):
+            d = I.config5(M, N, K)
+            a, bias = d["A"].cuda(), d["bias"].cuda()
+            bp = RT.fp8_pack_b(d["B"].cuda())
+            out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            return lambda: RT.fp8_gemm_packed(a, bp, N, bias=bias, out=out, act="silu", scale_a=d["scale_a"],
+                                              scale_b=d["scale_b"])
+        return make
+
+    dec_shapes = [(16, 4096, 4096)] if quick else [
+        (m, n, k) for m in (16, 32) for (n, k) in ((4096, 4096), (11008, 4096), (4096, 11008))]
+    for (M, N, K) in dec_shapes:
+        record_rows("fp8_gemm_bias_silu_packed", dict(M=M, N=N, K=K), "fp8", _decode(M, N, K),
+                    M * K + K * N + 4 * N + 2 * M * N)
     return rows
 
 
