@@ -45,7 +45,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves) __attribute__((amdgpu_waves
 fp8_decode_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ Bp, const float* __restrict__ bias,
                   __bf16* __restrict__ C, int M, int N, int K, float alpha) {
   typedef Mfma<DT_FP8, 16> Op;
-  constexpr int U = MT == 1 ? kDecodeUnroll : kDecodeUnroll / 2;  // steps per group: fragments in registers
+  constexpr int U = kDecodeUnroll;  // steps per group, their fragments all in registers  // steps per group: fragments in registers
   const int nb = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int S = K >> 7;
