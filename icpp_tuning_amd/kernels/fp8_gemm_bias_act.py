@@ -66,4 +66,31 @@ def build_kernel(M, N, K, config=None, act: str = "silu"):
     return CompiledFp8Gemm(d, M, N, K, config, act=act)
 
 
-__all__ = ["DESCRIPTOR", "Fp8GemmBiasActDescriptor", "build_kernel", "get_configs"]
+class PackedFp8Decode:
+    """``kernel(a_q, scale_a, scale_b, bias) -> act(scale_a*scale_b * a_q @ b_q + bias)`` for
+    M <= 32 rows per call, with b_q [K, N] packed once at construction (icpp_fp8_pack_b)
+    and every call one launch of icpp_fp8_gemm_packed: for weights that stay fixed across
+    calls (decode), where the tiled path needs split-K plus a reduce launch."""
+
+    def __init__(self, b_q: torch.Tensor, act: str = "silu"):
+        from .. import runtime
+
+        self.K, self.N = b_q.shape
+        self.act = act
+        self.packed = runtime.fp8_pack_b(b_q)
+
+    def __call__(self, a_q, scale_a, scale_b, bias=None, out=None):
+        from .. import runtime
+
+        return runtime.fp8_gemm_packed(a_q, self.packed, self.N, bias=bias, out=out, act=self.act,
+                                       scale_a=float(scale_a), scale_b=float(scale_b))
+
+
+def build_packed_kernel(b_q: torch.Tensor, act: str = "silu") -> PackedFp8Decode:
+    """The decode kernel over pre-packed weights (see PackedFp8Decode); needs K % 128 == 0
+    and N % 16 == 0."""
+    return PackedFp8Decode(b_q, act=act)
+
+
+__all__ = ["DESCRIPTOR", "Fp8GemmBiasActDescriptor", "PackedFp8Decode", "build_kernel", "build_packed_kernel",
+           "get_configs"]

@@ -106,3 +106,15 @@ def test_decode_in_a_graph(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {rep}"
         _ = (a.float() * 2).sum().item()  # eager work between replays
+
+
+def test_build_packed_kernel(gpu):
+    """The module-level wrapper: weights packed once at build time, then calls like the
+    tiled kernel's (a_q, scale_a, scale_b, bias)."""
+    M, N, K = 9, 512, 1024
+    d = I.config5(M, N, K)
+    ref = O.fp8_gemm_bias_act_ref(d["A"], d["B"], d["scale_a"], d["scale_b"], d["bias"], "silu")
+    k = fp8_mod.build_packed_kernel(d["B"].cuda())
+    y = k(d["A"].cuda(), d["scale_a"], d["scale_b"], d["bias"].cuda())
+    torch.cuda.synchronize()
+    _close(y, ref, 1e-2, 1e-2, "build_packed_kernel")
