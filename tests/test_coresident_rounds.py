@@ -132,3 +132,34 @@ def test_the_model_catches_a_map_that_splits_row_blocks_across_rounds():
             simulate(32, 16, 256, 16, 2, 4, 0)
     finally:
         cr_item = keep
+
+
+def test_statistics_split_stays_inside_two_stage_arrays():
+    """For every f16 GEMM tile and row width the co-resident strategy accepts
+    (kernels/gemm_bias_layernorm.py coresident_fits, the launcher's own check), the
+    kernel's split of a row block's [rows][tiles_n] (mean, M2) pairs -- an even r0 =
+    min(rows, per & ~1) rows in the first stage array, the rest in the second, per =
+    stage bytes / (8 tiles_n) -- keeps both parts inside one stage array each for every
+    row count of a (possibly ragged) row block, and the first part ends on a 16-byte
+    boundary (no 16-byte load straddles the arrays)."""
+    from icpp_tuning_amd.kernels import gemm_bias_layernorm as ln
+    from icpp_tuning_amd.kernels._base import family_instances
+
+    checked = 0
+    for inst in family_instances("gemm"):
+        if inst.dtype != "f16":
+            continue
+        stage = (inst.bm + inst.bn) * inst.bk * 2
+        for N in (8, 128, 776, 1024, 2304, 2312, 4096, 8192, 11008, 16384, 32768):
+            if not ln.coresident_fits(inst, N):
+                continue
+            tiles_n = -(-N // inst.bn)
+            rowb = 8 * tiles_n
+            per = stage // rowb
+            for rows in range(1, inst.bm + 1):
+                r0 = min(rows, per & ~1)
+                assert r0 % 2 == 0 or r0 == rows, (inst.name, N, rows)
+                assert r0 * rowb <= stage and (rows - r0) * rowb <= stage, (inst.name, N, rows)
+                assert (r0 * tiles_n) % 2 == 0 or r0 == rows   # nvec0 = r0 * tiles_n / 2 exact
+            checked += 1
+    assert checked > 100
